@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""Benchmark of the KV-cache data path on one MI355X.
+
+One bench step is one whole handoff-and-decode job on synthetic data of the
+Llama-3-8B shape (32 layers, 8 KV / 32 query heads, head_dim 128, bf16,
+batch 64, prompt lengths U[128, 8192] seeded): pack every layer's live rows
+into the handoff buffer, unpack them into the decode cache, then 256 decode
+steps of fused KV append + single-query GQA attention over all 32 layers.
+Inputs are resident in HBM before the timed region.
+
+Prints one JSON line: ``value`` = pack+unpack GB/s (algorithmic bytes), with
+the decode append+attend time per step, the roofline of the dominant kernel
+(decode attention) and the CPU baseline (the reference's PyTorch ops on this
+host's cores, on a bounded sample of the same workload).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from hexgen2_amd import ops  # noqa: E402
+from hexgen2_amd.workloads import WORKLOADS, workload  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "KV pack+unpack GB/s (% HBM peak); decode append+attend µs/step at Llama-3-8B"
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Job:
+    """Device buffers of one workload and the timed job pass."""
+
+    def __init__(self, w, device):
+        self.w = w
+        L, B, S = w.layers, w.batch, w.capacity
+        shape = (L, B, S, 2, w.kv_heads, w.head_dim)
+        g = torch.Generator(device=device).manual_seed(w.seed + 1)
+        self.prefill = torch.empty(shape, dtype=w.dtype, device=device)
+        for l in range(L):  # K/V ~ N(0, 1)
+            self.prefill[l].normal_(generator=g)
+        self.packed = torch.empty((L, w.live_rows, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=device)
+        self.decode = torch.empty(shape, dtype=w.dtype, device=device)
+        self.prefill_layers = list(self.prefill.unbind(0))
+        self.decode_layers = list(self.decode.unbind(0))
+        self.q = torch.randn((L, B, 1, w.q_heads, w.head_dim), generator=g, device=device).to(w.dtype)
+        self.kv_new = torch.randn((L, B, 2, w.kv_heads, w.head_dim), generator=g, device=device).to(w.dtype)
+        self.out = torch.empty((B, 1, w.q_heads, w.head_dim), dtype=w.dtype, device=device)
+        self.seqlens = torch.tensor(w.lens, dtype=torch.int32, device=device)
+        self.max_len = max(w.lens)
+        self.plan = ops.AttendPlan(self.q[0], self.decode_layers[0], self.out,
+                                   max_seqlens=[self.max_len + t + 1 for t in range(w.decode_steps)],
+                                   seqlens=self.seqlens, kv_new=self.kv_new[0])
+        torch.cuda.synchronize()
+
+    def run(self, events=None):
+        """pack -> unpack -> decode steps; records (pack, unpack, step...) events."""
+        w = self.w
+        ev = events
+        if ev is not None:
+            ev[0].record()
+        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
+        if ev is not None:
+            ev[1].record()
+        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        if ev is not None:
+            ev[2].record()
+        for t in range(w.decode_steps):
+            for l in range(w.layers):
+                self.plan(self.q[l], self.decode_layers[l], self.out, self.kv_new[l], t, self.max_len + t + 1)
+            if ev is not None:
+                ev[3 + t].record()
+
+    def verify(self):
+        """Size-independent self-check on the full workload: the unpacked live
+        rows equal the prefill cache's (before any append) and the packed
+        buffer is the concatenation of live rows; checked on the device."""
+        w = self.w
+        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
+        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        start = 0
+        for b, n in enumerate(w.lens):
+            a = self.prefill[:, b, :n]
+            if not torch.equal(a, self.decode[:, b, :n]) or not torch.equal(a, self.packed[:, start:start + n]):
+                raise AssertionError(f"pack/unpack round trip differs for sequence {b}")
+            start += n
+
+
+def cpu_baseline(w, job, budget_s):
+    """The reference's PyTorch ops (oracle/cpu_path.py) on host cores, on a
+    bounded sample: 2 layers of pack+unpack and 1 layer x a few decode steps
+    of append+attend, at full batch; scaled to the full workload."""
+    from oracle import cpu_path
+
+    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(cores)
+    n_layers = min(2, w.layers)
+    layers = [job.prefill[l].cpu() for l in range(n_layers)]
+    t0 = time.perf_counter()
+    packed = cpu_path.pack(layers, w.lens)
+    t1 = time.perf_counter()
+    decode = cpu_path.unpack(packed, w.capacity, w.lens)
+    t2 = time.perf_counter()
+    pu_bytes = 4 * n_layers * w.live_rows * w.row_bytes
+    pu_gbs = pu_bytes / (t2 - t0) / 1e9
+    q = job.q[0].cpu()
+    kv = job.kv_new[0].cpu()
+    steps, step_times = 0, []
+    deadline = time.perf_counter() + budget_s
+    while steps < min(4, w.decode_steps) and (steps == 0 or time.perf_counter() < deadline):
+        s0 = time.perf_counter()
+        cpu_path.append(decode[0], kv, [n + steps for n in w.lens])
+        cpu_path.attend(q, decode[0], [n + steps + 1 for n in w.lens])
+        step_times.append(time.perf_counter() - s0)
+        steps += 1
+    layer_step = statistics.median(step_times)
+    sample = (f"{n_layers} layers pack+unpack ({pu_bytes / 1e9:.2f} GB) and {steps} decode steps x 1 layer "
+              f"of append+attend, batch {w.batch}; decode scaled x{w.layers} layers")
+    return {"value": round(pu_gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": sample, "decode_ms_per_step": round(layer_step * w.layers * 1e3, 1),
+            "pack_s": round(t1 - t0, 3), "unpack_s": round(t2 - t1, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="llama3-8b", choices=WORKLOADS)
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-verify", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the KV path here runs prefill and decode on one "
+              "MI355X; run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    w = workload(args.workload)
+    log(f"workload {w.describe()}")
+    job = Job(w, device)
+    log("buffers ready")
+    if not args.no_verify:
+        job.verify()
+        log("full-size pack/unpack round trip verified")
+
+    n_ev = 3 + w.decode_steps
+    for _ in range(args.warmup):
+        job.run()
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    pu_times, pack_times, decode_steps_ms, wall = [], [], [], []
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for k in range(args.steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+        job.run(ev)
+        torch.cuda.synchronize()
+        pack_times.append(ev[0].elapsed_time(ev[1]))
+        pu_times.append(ev[0].elapsed_time(ev[2]))
+        decode_steps_ms.extend(ev[2 + t].elapsed_time(ev[3 + t]) for t in range(w.decode_steps))
+        log(f"step {k}: pack+unpack {pu_times[-1]:.3f} ms, decode {ev[2].elapsed_time(ev[-1]):.1f} ms")
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+
+    pu_ms = statistics.median(pu_times)
+    pu_gbs = w.pack_unpack_bytes() / (pu_ms * 1e-3) / 1e9
+    decode_total_ms = sum(decode_steps_ms) / args.steps
+    decode_us_step = decode_total_ms / w.decode_steps * 1e3
+    decode_gbs = w.decode_bytes() / (decode_total_ms * 1e-3) / 1e9
+    launch_bytes = w.decode_bytes() / (w.layers * w.decode_steps)
+    attend_us = decode_total_ms * 1e3 / (w.layers * w.decode_steps)
+    traffic = None
+    if TRAFFIC_FILE.is_file():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get(w.name, {}).get("attend_bytes_per_launch")
+    result = {
+        "metric": METRIC,
+        "value": round(pu_gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": str(w.dtype).split(".")[-1].replace("bfloat16", "bf16").replace("float16", "fp16"),
+        "data": "synthetic (seeded N(0,1) K/V, seeded ragged lengths)",
+        "config": {**w.describe(), "parallelism": "single GPU (prefill and decode share it)"},
+        "pack_unpack_ms": round(pu_ms, 3),
+        "pack_unpack_hbm_frac": round(pu_gbs / HBM_PEAK_GBS, 4),
+        "pack_ms": round(statistics.median(pack_times), 3),
+        "decode_append_attend_us_per_step": round(decode_us_step, 1),
+        "decode_gbs": round(decode_gbs, 1),
+        "decode_hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "kernel": "attend_kernel + combine_kernel (fused append+attend, one layer)",
+            "bound": "hbm",
+            "achieved": round(launch_bytes / (attend_us * 1e-6) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(launch_bytes / (attend_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": int(launch_bytes),
+            "avg_launch_us": round(attend_us, 2),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(w, job, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,85 @@
+"""ctypes binding of ``libhexkv.so`` (the C ABI declared in ``include/hexkv.h``).
+
+The library is built in tree by ``python -m hexgen2_amd.build``.  Loading it
+fails loudly when it is missing: there is no CPU fallback for the data path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parent / "libhexkv.so"
+
+HEXKV_F16, HEXKV_BF16, HEXKV_F32 = 0, 1, 2
+HEXKV_OK = 0
+HEXKV_EINVAL, HEXKV_ERANGE, HEXKV_EHIP, HEXKV_EUNSUPPORTED, HEXKV_EWORKSPACE = -1, -2, -3, -4, -5
+MAX_LAYERS_PER_LAUNCH = 96
+MAX_SEQS_PER_LAUNCH = 256
+
+# Every symbol the header declares; tests check the library exports them all.
+EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "hexkv_append",
+           "hexkv_attend_workspace_bytes", "hexkv_attend")
+
+
+class AttendParams(ctypes.Structure):
+    """Mirror of ``hexkv_attend_params``."""
+    _fields_ = [
+        ("dtype", ctypes.c_int), ("batch", ctypes.c_int), ("q_len", ctypes.c_int),
+        ("q_heads", ctypes.c_int), ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+        ("causal", ctypes.c_int), ("softmax_scale", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("q_batch_stride", ctypes.c_int64), ("q_row_stride", ctypes.c_int64),
+        ("cache", ctypes.c_void_p), ("cache_batch_stride", ctypes.c_int64),
+        ("cache_pos_stride", ctypes.c_int64), ("cache_kv_stride", ctypes.c_int64),
+        ("capacity", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("out_batch_stride", ctypes.c_int64), ("out_row_stride", ctypes.c_int64),
+        ("seqlens_dev", ctypes.c_void_p), ("seqlen_bias", ctypes.c_int32), ("max_seqlen", ctypes.c_int32),
+        ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int),
+    ]
+
+
+class HexKVError(RuntimeError):
+    """A HIP runtime failure reported by the library."""
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the built library once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIBRARY.is_file():
+        raise RuntimeError(f"{LIBRARY} is missing: build it with `python -m hexgen2_amd.build` "
+                           "(the KV data path has no CPU fallback)")
+    lib = ctypes.CDLL(str(LIBRARY))
+    vp, i64, i32, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int
+    ptrs = ctypes.POINTER(ctypes.c_void_p)
+    lib.hexkv_version.restype = ci
+    lib.hexkv_version.argtypes = []
+    lib.hexkv_last_error.restype = ctypes.c_char_p
+    lib.hexkv_last_error.argtypes = []
+    for name in ("hexkv_pack", "hexkv_unpack"):
+        fn = getattr(lib, name)
+        fn.restype = ci
+        fn.argtypes = [ptrs, ptrs, ci, ci, i64, i64, i64, ctypes.POINTER(i64), vp]
+    lib.hexkv_append.restype = ci
+    lib.hexkv_append.argtypes = [vp, vp, ci, i64, i64, i64, vp, i32, vp]
+    lib.hexkv_attend_workspace_bytes.restype = ctypes.c_size_t
+    lib.hexkv_attend_workspace_bytes.argtypes = [ctypes.POINTER(AttendParams)]
+    lib.hexkv_attend.restype = ci
+    lib.hexkv_attend.argtypes = [ctypes.POINTER(AttendParams), vp, ctypes.c_size_t, vp]
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a hexkv status to the exception type the reference raises for it."""
+    if rc == HEXKV_OK:
+        return
+    message = f"{what}: {load().hexkv_last_error().decode()}"
+    if rc in (HEXKV_EINVAL, HEXKV_ERANGE, HEXKV_EWORKSPACE):
+        raise ValueError(message)
+    if rc == HEXKV_EUNSUPPORTED:
+        raise NotImplementedError(message)
+    raise HexKVError(message)

@@ -1,0 +1,227 @@
+// Ragged live-position copies of the KV-cache handoff: pack (cache -> packed
+// handoff buffer), unpack (packed -> decode cache) and per-step append.
+//
+// All three are pure byte movement, bound by HBM bandwidth.  Design for gfx950:
+//  * one launch covers every layer of a request (grid.y = layer) and every
+//    sequence of the batch; the per-sequence row offsets (prefix sums of the
+//    live lengths) and the per-layer base pointers travel in the kernel
+//    arguments, so no metadata is read from HBM and no padded row is moved;
+//  * grid.x tiles each layer's packed region into fixed-size byte chunks, so
+//    work per workgroup is uniform however ragged the lengths are; a chunk
+//    crosses at most a few sequence boundaries, found by one scalar binary
+//    search per workgroup;
+//  * each lane moves 16-byte vectors with nontemporal (streaming) loads and
+//    stores, four in flight per lane, so the 256 MB MALL is not polluted by
+//    data that is touched exactly once.
+#include "hexkv_common.h"
+
+#include <algorithm>
+
+namespace hexkv {
+
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 4;
+
+struct RaggedCopyArgs {
+  const char *src[HEXKV_MAX_LAYERS_PER_LAUNCH];
+  char *dst[HEXKV_MAX_LAYERS_PER_LAUNCH];
+  int64_t row_bytes;
+  int64_t seq_stride_bytes;  // padded (cache) side: bytes between sequences
+  int64_t chunk_bytes;       // packed bytes per workgroup
+  int64_t layer_bytes;       // packed bytes per layer in this launch
+  int32_t batch;
+  int32_t cu[HEXKV_MAX_SEQS_PER_LAUNCH + 1];  // packed row offset of each sequence
+};
+
+template <typename V>
+__device__ __forceinline__ void copy_span(const char *__restrict__ s, char *__restrict__ d,
+                                          int64_t n) {
+  const V *sv = reinterpret_cast<const V *>(s);
+  V *dv = reinterpret_cast<V *>(d);
+  const int64_t nv = n / static_cast<int64_t>(sizeof(V));
+  int64_t i = threadIdx.x;
+  for (; i + (kCopyUnroll - 1) * kCopyThreads < nv; i += kCopyUnroll * kCopyThreads) {
+    V r[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) r[u] = __builtin_nontemporal_load(sv + i + u * kCopyThreads);
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) __builtin_nontemporal_store(r[u], dv + i + u * kCopyThreads);
+  }
+  for (; i < nv; i += kCopyThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(sv + i), dv + i);
+}
+
+// PACK: src = padded cache, dst = packed buffer.  UNPACK: the reverse.
+template <typename V, bool PACK>
+__global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const RaggedCopyArgs a) {
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * a.chunk_bytes;
+  if (start >= a.layer_bytes) return;
+  const int64_t end = min(start + a.chunk_bytes, a.layer_bytes);
+  const char *src = a.src[blockIdx.y];
+  char *dst = a.dst[blockIdx.y];
+  const int64_t row = a.row_bytes;
+  // Last sequence whose packed range starts at or before `start`.
+  int lo = 0, hi = a.batch;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(a.cu[mid]) * row <= start) lo = mid; else hi = mid;
+  }
+  for (int b = lo; b < a.batch; ++b) {
+    const int64_t seg0 = static_cast<int64_t>(a.cu[b]) * row;
+    if (seg0 >= end) break;
+    const int64_t seg1 = static_cast<int64_t>(a.cu[b + 1]) * row;
+    const int64_t p0 = max(start, seg0), p1 = min(end, seg1);
+    if (p0 >= p1) continue;
+    const int64_t padded = static_cast<int64_t>(b) * a.seq_stride_bytes + (p0 - seg0);
+    if constexpr (PACK) copy_span<V>(src + padded, dst + p0, p1 - p0);
+    else copy_span<V>(src + p0, dst + padded, p1 - p0);
+  }
+}
+
+template <typename V>
+__global__ __launch_bounds__(kCopyThreads) void append_kernel(
+    const char *__restrict__ kv_new, char *__restrict__ cache, int64_t seq_stride_bytes,
+    int64_t capacity, int64_t row_bytes, const int32_t *__restrict__ positions, int32_t bias) {
+  const int b = blockIdx.y;
+  const int64_t pos = (positions ? static_cast<int64_t>(positions[b]) : 0) + bias;
+  if (pos < 0 || pos >= capacity) return;
+  const int64_t nv = row_bytes / static_cast<int64_t>(sizeof(V));
+  const V *s = reinterpret_cast<const V *>(kv_new + b * row_bytes);
+  V *d = reinterpret_cast<V *>(cache + b * seq_stride_bytes + pos * row_bytes);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kCopyThreads + threadIdx.x; i < nv;
+       i += static_cast<int64_t>(gridDim.x) * kCopyThreads)
+    d[i] = s[i];
+}
+
+// ------------------------------------------------------------------ host ---
+
+// Packed bytes per workgroup: large enough to amortise the per-workgroup
+// sequence search, small enough to give every CU many workgroups.
+static int64_t choose_chunk(int64_t total_bytes) {
+  const int64_t target_wgs = 8192;
+  int64_t chunk = (total_bytes / target_wgs + 4095) / 4096 * 4096;
+  return std::min<int64_t>(std::max<int64_t>(chunk, 16384), 262144);
+}
+
+static int ragged_copy(bool pack, const void *const *src_layers, void *const *dst_layers,
+                       int n_layers, int batch, int64_t seq_stride_rows, int64_t capacity,
+                       int64_t row_bytes, const int64_t *lens, hipStream_t stream) {
+  clear_error();
+  const char *what = pack ? "hexkv_pack" : "hexkv_unpack";
+  if (n_layers < 0 || batch < 0) return fail(HEXKV_EINVAL, "%s: negative layer count or batch", what);
+  if (n_layers == 0 || batch == 0) return HEXKV_OK;
+  if (!src_layers || !dst_layers || !lens) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  if (row_bytes <= 0 || row_bytes % 4 != 0)
+    return fail(HEXKV_EINVAL, "%s: row_bytes %lld is not a positive multiple of 4", what,
+                static_cast<long long>(row_bytes));
+  if (capacity < 0 || (batch > 1 && seq_stride_rows < capacity) || seq_stride_rows < 0)
+    return fail(HEXKV_EINVAL, "%s: sequence stride %lld rows is below capacity %lld", what,
+                static_cast<long long>(seq_stride_rows), static_cast<long long>(capacity));
+  int64_t total_rows = 0;
+  for (int b = 0; b < batch; ++b) {
+    if (lens[b] < 0 || lens[b] > capacity)
+      return fail(HEXKV_ERANGE, "%s: length %lld of sequence %d outside [0, %lld]", what,
+                  static_cast<long long>(lens[b]), b, static_cast<long long>(capacity));
+    total_rows += lens[b];
+  }
+  if (total_rows > INT32_MAX) return fail(HEXKV_ERANGE, "%s: more than 2^31-1 live rows", what);
+  if (total_rows == 0) return HEXKV_OK;
+  bool vec16 = row_bytes % 16 == 0;
+  for (int l = 0; l < n_layers; ++l) {
+    if (!src_layers[l] || !dst_layers[l]) return fail(HEXKV_EINVAL, "%s: null layer pointer %d", what, l);
+    if ((reinterpret_cast<uintptr_t>(src_layers[l]) | reinterpret_cast<uintptr_t>(dst_layers[l])) & 3)
+      return fail(HEXKV_EINVAL, "%s: layer %d pointer not 4-byte aligned", what, l);
+    vec16 = vec16 && aligned16(src_layers[l]) && aligned16(dst_layers[l]);
+  }
+  const int64_t chunk = choose_chunk(total_rows * row_bytes * n_layers);
+
+  // Sequences in groups of HEXKV_MAX_SEQS_PER_LAUNCH, layers in groups of
+  // HEXKV_MAX_LAYERS_PER_LAUNCH; one launch per (group, group) pair.
+  int64_t row_base = 0;
+  for (int b0 = 0; b0 < batch; b0 += HEXKV_MAX_SEQS_PER_LAUNCH) {
+    const int nb = std::min(batch - b0, HEXKV_MAX_SEQS_PER_LAUNCH);
+    RaggedCopyArgs a;
+    a.row_bytes = row_bytes;
+    a.seq_stride_bytes = seq_stride_rows * row_bytes;
+    a.chunk_bytes = chunk;
+    a.batch = nb;
+    a.cu[0] = 0;
+    for (int b = 0; b < nb; ++b) a.cu[b + 1] = a.cu[b] + static_cast<int32_t>(lens[b0 + b]);
+    a.layer_bytes = static_cast<int64_t>(a.cu[nb]) * row_bytes;
+    const int64_t padded_off = static_cast<int64_t>(b0) * seq_stride_rows * row_bytes;
+    const int64_t packed_off = row_base * row_bytes;
+    row_base += a.cu[nb];
+    if (a.layer_bytes == 0) continue;
+    const int64_t gx = (a.layer_bytes + chunk - 1) / chunk;
+    if (gx > INT32_MAX) return fail(HEXKV_ERANGE, "%s: grid too large", what);
+    for (int l0 = 0; l0 < n_layers; l0 += HEXKV_MAX_LAYERS_PER_LAUNCH) {
+      const int nl = std::min(n_layers - l0, HEXKV_MAX_LAYERS_PER_LAUNCH);
+      for (int l = 0; l < nl; ++l) {
+        const char *s = static_cast<const char *>(src_layers[l0 + l]);
+        char *d = static_cast<char *>(dst_layers[l0 + l]);
+        a.src[l] = s + (pack ? padded_off : packed_off);
+        a.dst[l] = d + (pack ? packed_off : padded_off);
+      }
+      dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(nl));
+      if (vec16) {
+        if (pack) ragged_copy_kernel<u32x4, true><<<grid, kCopyThreads, 0, stream>>>(a);
+        else ragged_copy_kernel<u32x4, false><<<grid, kCopyThreads, 0, stream>>>(a);
+      } else {
+        if (pack) ragged_copy_kernel<unsigned int, true><<<grid, kCopyThreads, 0, stream>>>(a);
+        else ragged_copy_kernel<unsigned int, false><<<grid, kCopyThreads, 0, stream>>>(a);
+      }
+      int rc = check_launch(what);
+      if (rc != HEXKV_OK) return rc;
+    }
+  }
+  return HEXKV_OK;
+}
+
+}  // namespace hexkv
+
+extern "C" int hexkv_pack(const void *const *cache_layers, void *const *packed_layers, int n_layers,
+                          int batch, int64_t seq_stride_rows, int64_t capacity, int64_t row_bytes,
+                          const int64_t *lens, hexkv_stream_t stream) {
+  return hexkv::ragged_copy(true, cache_layers, packed_layers, n_layers, batch, seq_stride_rows,
+                            capacity, row_bytes, lens, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hexkv_unpack(const void *const *packed_layers, void *const *cache_layers,
+                            int n_layers, int batch, int64_t seq_stride_rows, int64_t capacity,
+                            int64_t row_bytes, const int64_t *lens, hexkv_stream_t stream) {
+  return hexkv::ragged_copy(false, packed_layers, cache_layers, n_layers, batch, seq_stride_rows,
+                            capacity, row_bytes, lens, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int hexkv_append(const void *kv_new, void *cache, int batch, int64_t seq_stride_rows,
+                            int64_t capacity, int64_t row_bytes, const int32_t *positions_dev,
+                            int32_t position_bias, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  if (batch < 0) return fail(HEXKV_EINVAL, "hexkv_append: negative batch");
+  if (batch == 0) return HEXKV_OK;
+  if (!kv_new || !cache) return fail(HEXKV_EINVAL, "hexkv_append: null argument");
+  if (row_bytes <= 0 || row_bytes % 4 != 0)
+    return fail(HEXKV_EINVAL, "hexkv_append: row_bytes %lld is not a positive multiple of 4",
+                static_cast<long long>(row_bytes));
+  if (capacity <= 0 || (batch > 1 && seq_stride_rows < capacity))
+    return fail(HEXKV_EINVAL, "hexkv_append: bad capacity/stride");
+  if (batch > 65535) return fail(HEXKV_EINVAL, "hexkv_append: batch above 65535");
+  if (!positions_dev && (position_bias < 0 || position_bias >= capacity))
+    return fail(HEXKV_ERANGE, "hexkv_append: position %d outside [0, %lld)", position_bias,
+                static_cast<long long>(capacity));
+  if ((reinterpret_cast<uintptr_t>(kv_new) | reinterpret_cast<uintptr_t>(cache)) & 3)
+    return fail(HEXKV_EINVAL, "hexkv_append: pointers not 4-byte aligned");
+  const bool vec16 = row_bytes % 16 == 0 && aligned16(kv_new) && aligned16(cache);
+  const int64_t nv = row_bytes / (vec16 ? 16 : 4);
+  const unsigned gx = static_cast<unsigned>(std::min<int64_t>((nv + kCopyThreads - 1) / kCopyThreads, 64));
+  dim3 grid(gx, static_cast<unsigned>(batch));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t stride = seq_stride_rows * row_bytes;
+  if (vec16)
+    append_kernel<u32x4><<<grid, kCopyThreads, 0, s>>>(static_cast<const char *>(kv_new),
+        static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias);
+  else
+    append_kernel<unsigned int><<<grid, kCopyThreads, 0, s>>>(static_cast<const char *>(kv_new),
+        static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias);
+  return check_launch("hexkv_append");
+}

@@ -1,0 +1,110 @@
+"""Drop-in replacements for the KV-cache calls of hexgen_core's attention module.
+
+* ``_update_kv_cache(kv, inference_params, layer_idx)`` -- append (and the
+  prefill write) into the per-layer cache; hexgen/hexgen_core/modules/
+  mha.py:255-288.
+* ``allocate_inference_cache(...)`` -- the non-FT cache of
+  ``MHA.allocate_inference_cache`` (mha.py:414-428).
+* ``FlashCrossAttention`` -- the attention module the reference's MHA calls at
+  decode (mha.py:105-142); same constructor and ``forward`` signature.
+
+Every data movement and every attention runs as a hexkv HIP kernel; CPU
+tensors are rejected.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import ops
+
+
+def allocate_inference_cache(batch_size: int, max_seqlen: int, num_heads_kv: int, head_dim: int,
+                             dtype: torch.dtype, device) -> torch.Tensor:
+    """``torch.empty(batch, max_seqlen, 2, kv_heads, head_dim)`` (mha.py:418-420)."""
+    return torch.empty(batch_size, max_seqlen, 2, num_heads_kv, head_dim, dtype=dtype, device=device)
+
+
+def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torch.Tensor:
+    """kv: (batch, seqlen, 2, kv_heads, head_dim).  Writes kv at
+    ``[batch_size_offset:+batch, sequence_len_offset:+seqlen]`` of layer
+    ``layer_idx``'s cache (allocated on first use) and returns the view
+    ``cache[batch_start:batch_end, :sequence_end]`` (mha.py:255-288)."""
+    if inference_params.fused_ft_kernel:
+        raise NotImplementedError("the FasterTransformer cache layout is not supported")
+    num_heads, head_dim = kv.shape[-2:]
+    cache = inference_params.key_value_memory_dict.get(layer_idx)
+    if cache is None:
+        cache = allocate_inference_cache(inference_params.max_batch_size,
+                                         inference_params.max_sequence_len, num_heads, head_dim,
+                                         kv.dtype, kv.device)
+        inference_params.key_value_memory_dict[layer_idx] = cache
+    batch_start = inference_params.batch_size_offset
+    batch_end = batch_start + kv.shape[0]
+    sequence_start = inference_params.sequence_len_offset
+    sequence_end = sequence_start + kv.shape[1]
+    assert batch_end <= cache.shape[0]
+    assert sequence_end <= cache.shape[1]
+    kv = kv.contiguous()
+    target = cache[batch_start:batch_end]
+    if kv.shape[1] == 1:
+        ops.append_kv(target, kv.reshape(kv.shape[0], -1), position_bias=sequence_start)
+    elif kv.shape[1] > 1:
+        # A multi-position write (prefill) is an unpack of one packed layer with
+        # uniform lengths into the cache shifted by sequence_start rows.
+        ops.unpack_live([kv.reshape(-1)], [target[:, sequence_start:]], [kv.shape[1]] * kv.shape[0])
+    return cache[batch_start:batch_end, :sequence_end]
+
+
+class FlashCrossAttention(nn.Module):
+    """Scaled dot-product attention of q against a packed KV tensor.
+
+    Same interface as hexgen_core's FlashCrossAttention (mha.py:87-142):
+    q (B, Sq, H, D), kv (B, Sk, 2, H_k, D) -> (B, Sq, H, D), GQA when
+    H_k < H.  With ``causal`` and Sq > 1 query t sees keys < Sk - Sq + t + 1
+    (the prefill triangle when Sq == Sk).  float32 is accepted too (the
+    reference routes it to CrossAttention, mha.py:195-244).  Dropout is not
+    applied (inference only).
+    """
+
+    def __init__(self, causal=False, softmax_scale=None, attention_dropout=0.0):
+        super().__init__()
+        self.causal = causal
+        self.softmax_scale = softmax_scale
+        self.drop = nn.Dropout(attention_dropout)
+
+    def forward(self, q, kv, causal=None, cu_seqlens=None, max_seqlen=None,
+                cu_seqlens_k=None, max_seqlen_k=None):
+        assert q.dtype in (torch.float16, torch.bfloat16, torch.float32)
+        assert q.is_cuda and kv.is_cuda
+        if cu_seqlens is not None or cu_seqlens_k is not None:
+            raise NotImplementedError("variable-length (cu_seqlens) attention is not supported")
+        causal = self.causal if causal is None else causal
+        batch_size = q.shape[0]
+        seqlen_k = kv.shape[1]
+        assert kv.shape[0] == batch_size and kv.shape[4] == q.shape[3]
+        q = q if q.stride(-1) == 1 and q.stride(-2) == q.shape[-1] else q.contiguous()
+        if kv.stride(-1) != 1 or kv.stride(-2) != kv.shape[-1] or kv.stride(1) != kv[0, 0].numel():
+            kv = kv.contiguous()
+        return ops.decode_attention(q, kv, max_seqlen=seqlen_k, seqlen_bias=seqlen_k,
+                                    causal=bool(causal) and q.shape[1] > 1,
+                                    softmax_scale=self.softmax_scale)
+
+
+def update_and_attend(q: torch.Tensor, kv: torch.Tensor, inference_params, layer_idx: int,
+                      softmax_scale: Optional[float] = None) -> torch.Tensor:
+    """The decode-step pair ``_update_kv_cache`` + ``inner_cross_attn(q, kv,
+    causal=False)`` (mha.py:565-569) as one fused HIP launch: the new row is
+    written to the cache and attended from registers.  q (B, 1, H, D),
+    kv (B, 1, 2, H_k, D)."""
+    cache = inference_params.key_value_memory_dict[layer_idx]
+    batch_start = inference_params.batch_size_offset
+    batch_end = batch_start + kv.shape[0]
+    offset = inference_params.sequence_len_offset
+    assert kv.shape[1] == 1 and q.shape[1] == 1
+    assert batch_end <= cache.shape[0] and offset + 1 <= cache.shape[1]
+    target = cache[batch_start:batch_end]
+    return ops.decode_attention(q.contiguous(), target, max_seqlen=offset + 1, seqlen_bias=offset,
+                                kv_new=kv.contiguous(), softmax_scale=softmax_scale)

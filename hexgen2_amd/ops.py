@@ -1,0 +1,284 @@
+"""Tensor-level entry points of the KV data path, each one call into ``libhexkv.so``.
+
+All tensors live on the current HIP device (``torch.cuda`` on ROCm); work is
+enqueued on the current stream.  Shapes follow hexgen_core's cache layout
+``[batch, capacity, 2, kv_heads, head_dim]`` (hexgen/hexgen_core/modules/
+mha.py:260-265): one *row* is one position's K and V for every KV head.
+Lengths that size work (``lens``, ``max_seqlen``) are host integers and are
+validated on the host before anything is launched.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float16: _lib.HEXKV_F16, torch.bfloat16: _lib.HEXKV_BF16,
+           torch.float32: _lib.HEXKV_F32}
+
+TensorList = Union[torch.Tensor, Sequence[torch.Tensor]]
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError("hexkv operates on HIP device tensors only; the KV data path has "
+                             f"no CPU fallback (got a tensor on {t.device})")
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _row_geometry(cache: torch.Tensor):
+    """(row_elems, row_bytes, seq_stride_rows) of a ``[B, S, *row]`` cache."""
+    if cache.dim() < 3:
+        raise ValueError(f"cache must be [batch, capacity, *row], got shape {tuple(cache.shape)}")
+    row_elems = math.prod(cache.shape[2:])
+    inner = cache[0, 0] if cache.shape[0] and cache.shape[1] else None
+    if inner is not None and not inner.is_contiguous():
+        raise ValueError("cache rows (dims 2+) must be contiguous")
+    if cache.shape[1] > 1 and cache.stride(1) != row_elems:
+        raise ValueError("cache positions must be consecutive rows (stride(1) == row size)")
+    if cache.shape[0] > 1 and cache.stride(0) % row_elems:
+        raise ValueError("cache batch stride must be a whole number of rows")
+    seq_stride = cache.stride(0) // row_elems if cache.shape[0] > 1 else cache.shape[1]
+    return row_elems, row_elems * cache.element_size(), seq_stride
+
+
+def _as_layers(x: TensorList) -> list:
+    return list(x.unbind(0)) if isinstance(x, torch.Tensor) else list(x)
+
+
+def _check_lens(lens: Sequence[int], batch: int) -> list:
+    lens = [int(n) for n in lens]
+    if len(lens) != batch:
+        raise ValueError(f"{len(lens)} lengths for a batch of {batch}")
+    return lens
+
+
+def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, dtype, device):
+    layers = _as_layers(packed)
+    if len(layers) != n_layers:
+        raise ValueError(f"{len(layers)} packed layers for {n_layers} cache layers")
+    ptrs = []
+    for t in layers:
+        _require_device(t)
+        if t.dtype != dtype or t.device != device:
+            raise ValueError("packed and cache tensors differ in dtype or device")
+        if t.numel() != total * row_elems or not t.is_contiguous():
+            raise ValueError(f"packed layer must be contiguous with {total} rows of {row_elems} "
+                             f"elements, got shape {tuple(t.shape)}")
+        ptrs.append(t.data_ptr())
+    return ptrs
+
+
+def _cache_ptrs(cache_layers: TensorList):
+    layers = _as_layers(cache_layers)
+    if not layers:
+        raise ValueError("no cache layers")
+    first = layers[0]
+    _require_device(first)
+    geometry = _row_geometry(first)
+    for t in layers[1:]:
+        _require_device(t)
+        if t.shape != first.shape or t.dtype != first.dtype or t.device != first.device \
+                or t.stride() != first.stride():
+            raise ValueError("all cache layers must share shape, strides, dtype and device")
+    return first, layers, geometry
+
+
+def pack_live(cache_layers: TensorList, lens: Sequence[int],
+              out: Optional[TensorList] = None) -> TensorList:
+    """Gather rows ``[0, lens[b])`` of every sequence of every layer into the
+    packed handoff layout ``[n_layers, sum(lens), *row]`` (one launch).
+
+    Batch-1 form of hexgen2/model.py:81 ``t[:, :L].contiguous()`` per layer,
+    generalised to ragged batches.  ``out`` may be one ``[n_layers, T, *row]``
+    tensor or a list of per-layer contiguous tensors.
+    """
+    first, layers, (row_elems, row_bytes, seq_stride) = _cache_ptrs(cache_layers)
+    lens = _check_lens(lens, first.shape[0])
+    total = sum(lens)
+    if out is None:
+        out = torch.empty((len(layers), total, *first.shape[2:]), dtype=first.dtype,
+                          device=first.device)
+    dst = _packed_ptrs(out, len(layers), total, row_elems, first.dtype, first.device)
+    n = len(layers)
+    rc = _lib.load().hexkv_pack((ctypes.c_void_p * n)(*[t.data_ptr() for t in layers]),
+                                (ctypes.c_void_p * n)(*dst), n, len(lens), seq_stride,
+                                first.shape[1], row_bytes, (ctypes.c_int64 * len(lens))(*lens),
+                                _stream(first))
+    _lib.check(rc, "hexkv_pack")
+    return out
+
+
+def unpack_live(packed: TensorList, cache_layers: TensorList, lens: Sequence[int]) -> None:
+    """Scatter the packed handoff layout into preallocated caches: rows
+    ``[0, lens[b])`` of each sequence are overwritten, all other rows are
+    left untouched (hexgen2/model.py:104-108 writes into ``torch.empty``)."""
+    first, layers, (row_elems, row_bytes, seq_stride) = _cache_ptrs(cache_layers)
+    lens = _check_lens(lens, first.shape[0])
+    src = _packed_ptrs(packed, len(layers), sum(lens), row_elems, first.dtype, first.device)
+    n = len(layers)
+    rc = _lib.load().hexkv_unpack((ctypes.c_void_p * n)(*src),
+                                  (ctypes.c_void_p * n)(*[t.data_ptr() for t in layers]), n,
+                                  len(lens), seq_stride, first.shape[1], row_bytes,
+                                  (ctypes.c_int64 * len(lens))(*lens), _stream(first))
+    _lib.check(rc, "hexkv_unpack")
+
+
+def append_kv(cache: torch.Tensor, kv_new: torch.Tensor, positions: Optional[torch.Tensor] = None,
+              position_bias: int = 0) -> None:
+    """Write ``kv_new[b]`` (one row per sequence) into ``cache[b, pos_b]`` with
+    ``pos_b = positions[b] + position_bias`` (``positions`` a device int32
+    tensor, or None for a batch-uniform position): hexgen/hexgen_core/modules/
+    mha.py:286 with per-sequence offsets."""
+    _require_device(cache, kv_new)
+    row_elems, row_bytes, seq_stride = _row_geometry(cache)
+    batch = kv_new.shape[0]
+    if kv_new.dtype != cache.dtype or kv_new.device != cache.device:
+        raise ValueError("kv_new and cache differ in dtype or device")
+    if kv_new.numel() != batch * row_elems or not kv_new.is_contiguous():
+        raise ValueError(f"kv_new must be contiguous [batch, *row], got {tuple(kv_new.shape)}")
+    if batch > cache.shape[0]:
+        raise ValueError(f"batch {batch} exceeds the cache's {cache.shape[0]} sequences")
+    pos_ptr = None
+    if positions is not None:
+        _require_device(positions)
+        if positions.dtype != torch.int32 or positions.numel() < batch or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int32 device tensor with one entry per sequence")
+        pos_ptr = positions.data_ptr()
+    rc = _lib.load().hexkv_append(kv_new.data_ptr(), cache.data_ptr(), batch, seq_stride,
+                                  cache.shape[1], row_bytes, pos_ptr, int(position_bias),
+                                  _stream(cache))
+    _lib.check(rc, "hexkv_append")
+
+
+def _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, causal,
+                   softmax_scale, partition) -> _lib.AttendParams:
+    if q.dim() != 4 or cache.dim() != 5 or cache.shape[2] != 2:
+        raise ValueError("q must be [batch, q_len, q_heads, head_dim] and the cache "
+                         "[batch, capacity, 2, kv_heads, head_dim]")
+    batch, q_len, q_heads, head_dim = q.shape
+    if q.dtype not in _DTYPES or cache.dtype != q.dtype or out.dtype != q.dtype:
+        raise ValueError("q, cache and out must share one of float16, bfloat16, float32")
+    if cache.shape[0] < batch or cache.shape[4] != head_dim:
+        raise ValueError(f"cache shape {tuple(cache.shape)} does not fit q {tuple(q.shape)}")
+    kv_heads = cache.shape[3]
+    if q_heads % kv_heads:
+        raise ValueError("q_heads must be a multiple of kv_heads")
+    for name, t in (("q", q), ("out", out)):
+        if t.stride(3) != 1 or t.stride(2) != head_dim:
+            raise ValueError(f"{name} heads must be contiguous [.., heads, head_dim]")
+    if cache.stride(4) != 1 or cache.stride(3) != head_dim:
+        raise ValueError("cache heads must be contiguous [.., kv_heads, head_dim]")
+    p = _lib.AttendParams()
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.q_len, p.q_heads, p.kv_heads, p.head_dim = batch, q_len, q_heads, kv_heads, head_dim
+    p.causal = 1 if causal else 0
+    p.softmax_scale = float(head_dim ** -0.5 if softmax_scale is None else softmax_scale)
+    p.q, p.q_batch_stride, p.q_row_stride = q.data_ptr(), q.stride(0), q.stride(1)
+    p.cache = cache.data_ptr()
+    p.cache_batch_stride, p.cache_pos_stride, p.cache_kv_stride = cache.stride(0), cache.stride(1), cache.stride(2)
+    p.capacity = cache.shape[1]
+    p.out, p.out_batch_stride, p.out_row_stride = out.data_ptr(), out.stride(0), out.stride(1)
+    if seqlens is not None:
+        _require_device(seqlens)
+        if seqlens.dtype != torch.int32 or seqlens.numel() < batch or not seqlens.is_contiguous():
+            raise ValueError("seqlens must be a contiguous int32 device tensor")
+        p.seqlens_dev = seqlens.data_ptr()
+    p.seqlen_bias = int(seqlen_bias)
+    p.max_seqlen = int(max_seqlen)
+    if kv_new is not None:
+        _require_device(kv_new)
+        if kv_new.dtype != q.dtype or kv_new.numel() != batch * 2 * kv_heads * head_dim \
+                or not kv_new.is_contiguous():
+            raise ValueError("kv_new must be contiguous [batch, 2, kv_heads, head_dim]")
+        p.kv_new = kv_new.data_ptr()
+    p.partition = int(partition)
+    return p
+
+
+def attend_workspace_bytes(q: torch.Tensor, cache: torch.Tensor, max_seqlen: int,
+                           partition: int = 0) -> int:
+    out = q  # geometry only
+    p = _attend_params(q, cache, out, None, max_seqlen, max_seqlen, None, False, None, partition)
+    return int(_lib.load().hexkv_attend_workspace_bytes(ctypes.byref(p)))
+
+
+def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
+                     seqlens: Optional[torch.Tensor] = None, seqlen_bias: int = 0,
+                     kv_new: Optional[torch.Tensor] = None, causal: bool = False,
+                     softmax_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                     workspace: Optional[torch.Tensor] = None, partition: int = 0) -> torch.Tensor:
+    """Attention of ``q [B, q_len, Hq, D]`` over a cache ``[B, S, 2, Hkv, D]``.
+
+    Sequence b attends to ``len_b = seqlens[b] + seqlen_bias`` keys (the
+    uniform ``seqlen_bias`` alone when ``seqlens`` is None); with ``kv_new``
+    ``[B, 2, Hkv, D]`` the row is first appended at position ``len_b`` and
+    ``len_b + 1`` keys are attended.  ``max_seqlen`` is a host bound on the
+    attended length (including that +1).  GQA maps q head h to KV head
+    ``h // (Hq // Hkv)`` (mha.py:223-224); ``softmax_scale`` defaults to
+    ``D ** -0.5`` (gpt.py:72).
+    """
+    _require_device(q, cache)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    p = _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, causal,
+                       softmax_scale, partition)
+    lib = _lib.load()
+    need = int(lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        _require_device(workspace)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    rc = lib.hexkv_attend(ctypes.byref(p), ws_ptr, ws_bytes, _stream(q))
+    _lib.check(rc, "hexkv_attend")
+    return out
+
+
+class AttendPlan:
+    """Prebuilt ``hexkv_attend`` parameters for a decode loop on one geometry.
+
+    Building the parameter block once and patching only pointers, the length
+    bias and ``max_seqlen`` per call keeps host overhead per layer small; the
+    workspace is allocated once for the largest ``max_seqlen`` the loop will
+    use.  Arguments as for ``decode_attention``.
+    """
+
+    def __init__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *,
+                 max_seqlens: Sequence[int], seqlens: Optional[torch.Tensor] = None,
+                 kv_new: Optional[torch.Tensor] = None, softmax_scale: Optional[float] = None,
+                 partition: int = 0):
+        _require_device(q, cache, out)
+        self.params = _attend_params(q, cache, out, seqlens, 0, max(max_seqlens), kv_new, False,
+                                     softmax_scale, partition)
+        self.lib = _lib.load()
+        need = 0
+        for m in max_seqlens:
+            self.params.max_seqlen = int(m)
+            need = max(need, int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params))))
+        self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+        self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), self.workspace.numel()
+        self.stream = _stream(q)
+        self.shapes = (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype)
+
+    def __call__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
+                 kv_new: Optional[torch.Tensor], seqlen_bias: int, max_seqlen: int) -> torch.Tensor:
+        if (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype) != self.shapes:
+            raise ValueError("AttendPlan called with a different geometry")
+        p = self.params
+        p.q, p.cache, p.out = q.data_ptr(), cache.data_ptr(), out.data_ptr()
+        if kv_new is not None:
+            p.kv_new = kv_new.data_ptr()
+        p.seqlen_bias, p.max_seqlen = int(seqlen_bias), int(max_seqlen)
+        _lib.check(self.lib.hexkv_attend(ctypes.byref(p), self.ws_ptr, self.ws_bytes, self.stream),
+                   "hexkv_attend")
+        return out

@@ -1,0 +1,217 @@
+"""Self-describing tensor packets between the prefill and decode phases.
+
+Same entry points, header format and validation as the pilot's transport
+(hexgen2/transport.py:13-100): ``validate_header``, ``send_packet``,
+``recv_packet``, ``send_data``, ``recv_data``.  Two carriers:
+
+* ``DeviceChannel`` -- prefill and decode on the same GPU: the header is
+  encoded, size-checked and parsed exactly as on the wire, and the tensors
+  are handed over in device memory (no copy, no host round trip).  This is
+  the carrier of the KV handoff in this build.  The receiver gets the
+  sender's (contiguous) tensors; the sender must not modify them after
+  sending, which the pilot never does (run.py:146-177).
+* ``torch.distributed`` -- when no channel is active, packets use the
+  reference's wire protocol (int64 header length, UTF-8 JSON header, then one
+  send per non-empty tensor in header order), so a peer running the
+  reference transport interoperates.
+
+A channel is selected per call (``channel=``) or for a block of code
+(``with use_channel(endpoint):``).
+"""
+from __future__ import annotations
+
+import collections
+import contextlib
+import json
+import math
+import threading
+from typing import Optional
+
+import torch
+import torch.distributed as dist
+
+DTYPES = {str(dtype): dtype for dtype in (
+    torch.float16, torch.bfloat16, torch.float32, torch.float64,
+    torch.int64, torch.int32, torch.int16, torch.int8, torch.uint8, torch.bool,
+)}
+MAX_HEADER = 1024 * 1024
+MAX_PAYLOAD = 8 * 1024 ** 3
+MAX_TENSORS = 1024
+MAX_DIMS = 8
+
+_ELEMENT_BYTES = {name: torch.empty((), dtype=dtype).element_size() for name, dtype in DTYPES.items()}
+
+
+def validate_header(header, max_payload: int = MAX_PAYLOAD) -> int:
+    """Check a decoded packet header; returns its payload bytes.
+
+    Rejects (ValueError) what hexgen2/transport.py:25-41 rejects: a version
+    other than 1, a missing tensor list, more than 1024 tensors, duplicate or
+    non-string names, unknown dtypes, shapes that are not lists of at most 8
+    non-negative ints (bools are not ints here), and payloads above
+    ``max_payload`` (8 GiB on the wire).
+    """
+    if header.get("version") != 1 or not isinstance(header.get("tensors"), list):
+        raise ValueError("Unsupported tensor packet")
+    if len(header["tensors"]) > MAX_TENSORS:
+        raise ValueError("Too many tensors")
+    size, names = 0, set()
+    for item in header["tensors"]:
+        name, shape, dtype = item["name"], item["shape"], item["dtype"]
+        if not isinstance(name, str) or name in names or dtype not in DTYPES:
+            raise ValueError("Invalid tensor name or dtype")
+        if not isinstance(shape, list) or len(shape) > MAX_DIMS or any(
+                type(d) is not int or d < 0 for d in shape):
+            raise ValueError("Invalid tensor shape")
+        size += math.prod(shape) * _ELEMENT_BYTES[dtype]
+        names.add(name)
+    if size > max_payload:
+        raise ValueError("Tensor packet exceeds memory limit")
+    return size
+
+
+def _encode_header(tensors, metadata, max_payload):
+    header = {"version": 1, "metadata": metadata, "tensors": [
+        {"name": name, "shape": list(t.shape), "dtype": str(t.dtype)} for name, t in tensors.items()
+    ]}
+    payload_bytes = validate_header(header, max_payload)
+    encoded = json.dumps(header, allow_nan=False).encode("utf-8")
+    if not 0 < len(encoded) <= MAX_HEADER:
+        raise ValueError("Tensor metadata exceeds limit")
+    return encoded, payload_bytes
+
+
+def _decode_header(encoded: bytes, max_payload):
+    if not 0 < len(encoded) <= MAX_HEADER:
+        raise ValueError("Invalid tensor header length")
+    header = json.loads(encoded.decode("utf-8"))
+    validate_header(header, max_payload)
+    return header
+
+
+class DeviceChannel:
+    """One endpoint of an in-process, same-GPU packet channel.
+
+    ``a, b = DeviceChannel.pair()`` gives ranks 0 and 1; ``a`` sends to
+    ``dst=1`` and receives from ``src=1``.  Packets queue in order per
+    (src, dst).  ``max_payload`` bounds a packet (default: no bound beyond
+    device memory, since nothing is copied; the wire limit is 8 GiB).
+    """
+
+    def __init__(self, rank: int, mailboxes: dict, lock: threading.Lock,
+                 max_payload: Optional[int] = None):
+        self.rank = rank
+        self._mailboxes = mailboxes
+        self._lock = lock
+        self.max_payload = max_payload if max_payload is not None else 1 << 62
+
+    @classmethod
+    def pair(cls, max_payload: Optional[int] = None):
+        mailboxes = collections.defaultdict(collections.deque)
+        lock = threading.Lock()
+        return cls(0, mailboxes, lock, max_payload), cls(1, mailboxes, lock, max_payload)
+
+    def send(self, tensors, metadata, dst: int) -> int:
+        encoded, payload = _encode_header(tensors, metadata, self.max_payload)
+        items = [tensor.detach().contiguous() for tensor in tensors.values()]
+        with self._lock:
+            self._mailboxes[(self.rank, dst)].append((encoded, items))
+        return payload
+
+    def recv(self, src: int):
+        with self._lock:
+            box = self._mailboxes[(src, self.rank)]
+            if not box:
+                raise RuntimeError(f"no packet from rank {src} is waiting for rank {self.rank}")
+            encoded, items = box.popleft()
+        header = _decode_header(encoded, self.max_payload)
+        tensors = {}
+        for item, tensor in zip(header["tensors"], items):
+            if list(tensor.shape) != item["shape"] or str(tensor.dtype) != item["dtype"]:
+                raise ValueError("Packet tensor does not match its header")
+            tensors[item["name"]] = tensor
+        return tensors, header["metadata"]
+
+
+_active = threading.local()
+
+
+@contextlib.contextmanager
+def use_channel(channel: DeviceChannel):
+    """Route send_packet/recv_packet calls in this block through ``channel``."""
+    previous = getattr(_active, "channel", None)
+    _active.channel = channel
+    try:
+        yield channel
+    finally:
+        _active.channel = previous
+
+
+def _channel(channel):
+    return channel if channel is not None else getattr(_active, "channel", None)
+
+
+def wire_device():
+    """Device of wire tensors: the current GPU for NCCL/RCCL, else the CPU."""
+    return (torch.device("cuda", torch.cuda.current_device()) if dist.get_backend() == "nccl"
+            else torch.device("cpu"))
+
+
+def send_packet(tensors, metadata, dst, channel: Optional[DeviceChannel] = None):
+    """Send named tensors plus JSON metadata to ``dst``; returns payload bytes."""
+    channel = _channel(channel)
+    if channel is not None:
+        return channel.send(tensors, metadata, dst)
+    encoded, payload_bytes = _encode_header(tensors, metadata, MAX_PAYLOAD)
+    device = wire_device()
+    dist.send(torch.tensor([len(encoded)], dtype=torch.int64, device=device), dst=dst)
+    dist.send(torch.frombuffer(bytearray(encoded), dtype=torch.uint8).to(device), dst=dst)
+    for tensor in tensors.values():
+        tensor = tensor.detach().to(device).contiguous()
+        if tensor.numel():
+            dist.send(tensor, dst=dst)
+    return payload_bytes
+
+
+def recv_packet(src, channel: Optional[DeviceChannel] = None):
+    """Receive one packet from ``src``; returns (dict of tensors, metadata)."""
+    channel = _channel(channel)
+    if channel is not None:
+        return channel.recv(src)
+    device = wire_device()
+    length = torch.empty(1, dtype=torch.int64, device=device)
+    dist.recv(length, src=src)
+    size = int(length.item())
+    if not 0 < size <= MAX_HEADER:
+        raise ValueError("Invalid tensor header length")
+    encoded = torch.empty(size, dtype=torch.uint8, device=device)
+    dist.recv(encoded, src=src)
+    header = _decode_header(bytes(encoded.cpu().numpy().tobytes()), MAX_PAYLOAD)
+    tensors = {}
+    for item in header["tensors"]:
+        tensor = torch.empty(item["shape"], dtype=DTYPES[item["dtype"]], device=device)
+        if tensor.numel():
+            dist.recv(tensor, src=src)
+        tensors[item["name"]] = tensor
+    return tensors, header["metadata"]
+
+
+def send_data(single_tensor, tensor_dict, dst, channel: Optional[DeviceChannel] = None):
+    """Legacy API: a token tensor plus a KV dict keyed by int layer
+    (hexgen2/transport.py:83-90)."""
+    keys = list(tensor_dict)
+    if any(type(key) is not int for key in keys):
+        raise ValueError("KV-cache layer keys must be integers")
+    return send_packet({"token": single_tensor, **{f"kv/{key}": tensor_dict[key] for key in keys}},
+                       {"layers": keys}, dst, channel=channel)
+
+
+def recv_data(src, num_layers=None, tensor_shape=None, channel: Optional[DeviceChannel] = None):
+    """Legacy API counterpart of ``send_data`` (hexgen2/transport.py:93-100)."""
+    tensors, metadata = recv_packet(src, channel=channel)
+    cache = {key: tensors[f"kv/{key}"] for key in metadata["layers"]}
+    if num_layers is not None and len(cache) != num_layers:
+        raise ValueError("Received KV-cache layer count differs from expected count")
+    if tensor_shape is not None and any(tuple(t.shape) != tuple(tensor_shape) for t in cache.values()):
+        raise ValueError("Received KV-cache shape differs from expected shape")
+    return tensors["token"], cache

@@ -1,0 +1,189 @@
+/*
+ * hexkv.h -- C ABI of the MI355X (gfx950) KV-cache data path of HexGen-2's
+ * disaggregated prefill/decode pilot.
+ *
+ * Three steps, each a hand-written HIP kernel:
+ *   pack    gather the live positions of every layer's prefill cache into one
+ *           contiguous handoff buffer (ragged, prefix-sum offsets, no padding);
+ *   unpack  scatter that buffer into the decode phase's preallocated cache;
+ *   append  write the new token's K/V at each sequence's current length;
+ *   attend  single-query (GQA) attention over the cache, optionally with the
+ *           append fused in.
+ *
+ * Conventions (all entry points):
+ *   - Every pointer named *_dev or documented "device" is device memory on
+ *     the current HIP device; everything else is host memory read during the
+ *     call only.  The library never allocates device memory: callers own
+ *     every buffer, including the attention workspace.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *     and the call returns without synchronising.
+ *   - Return value: HEXKV_OK (0) or a negative hexkv_status.  A failed call
+ *     launches nothing; hexkv_last_error() then returns a message for the
+ *     calling thread.
+ *   - Cache layout (one layer): [batch][capacity][2][kv_heads][head_dim], the
+ *     layout hexgen_core allocates (hexgen/hexgen_core/modules/mha.py:260-265);
+ *     one "row" = one position's K and V for all KV heads = 2*Hkv*D*elem bytes.
+ *   - Packed (handoff) layout (one layer): [sum(lens)][row], sequences in batch
+ *     order, i.e. the per-sequence live slices of hexgen2/model.py:81 laid end
+ *     to end in send order (hexgen2/transport.py:56-59).
+ */
+#ifndef HEXKV_H_
+#define HEXKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *hexkv_stream_t; /* hipStream_t */
+
+enum hexkv_dtype {
+  HEXKV_F16 = 0,  /* torch.float16  */
+  HEXKV_BF16 = 1, /* torch.bfloat16 */
+  HEXKV_F32 = 2   /* torch.float32  */
+};
+
+enum hexkv_status {
+  HEXKV_OK = 0,
+  HEXKV_EINVAL = -1,       /* bad argument: shape, length, alignment, null */
+  HEXKV_ERANGE = -2,       /* a length or position exceeds the capacity    */
+  HEXKV_EHIP = -3,         /* the HIP runtime reported an error            */
+  HEXKV_EUNSUPPORTED = -4, /* valid request outside the compiled variants  */
+  HEXKV_EWORKSPACE = -5    /* workspace missing or too small               */
+};
+
+/* Largest layer count / batch one pack or unpack launch carries in its kernel
+ * arguments; larger requests are split into several launches by the library. */
+#define HEXKV_MAX_LAYERS_PER_LAUNCH 96
+#define HEXKV_MAX_SEQS_PER_LAUNCH 256
+
+/* Library version, major*10000 + minor*100 + patch. */
+int hexkv_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *hexkv_last_error(void);
+
+/*
+ * Pack: for every layer l < n_layers and sequence b < batch, copy rows
+ * [0, lens[b]) of sequence b of cache_layers[l] to packed_layers[l] at row
+ * offset lens[0] + ... + lens[b-1].
+ *
+ * Replaces the per-layer live-slice gather of Engine.prefill,
+ *   cache = {i: t[:, :len(input_ids)].contiguous() ...}  (hexgen2/model.py:81)
+ * generalised from batch 1 to a ragged batch, all layers in one launch.
+ *
+ *   cache_layers   host array [n_layers] of device pointers, each the base of
+ *                  one layer's cache [batch..][capacity][row]
+ *   packed_layers  host array [n_layers] of device pointers, each the base of
+ *                  that layer's packed region [sum(lens)][row]
+ *   seq_stride_rows  rows between consecutive sequences in the cache
+ *                  (= capacity for a [B][capacity][row] cache)
+ *   capacity       rows of one sequence in the cache; lens[b] <= capacity
+ *   row_bytes      bytes of one row; a multiple of 4
+ *   lens           host array [batch] of live lengths (0 allowed)
+ * Returns HEXKV_ERANGE if some lens[b] is negative or exceeds capacity.
+ */
+int hexkv_pack(const void *const *cache_layers, void *const *packed_layers,
+               int n_layers, int batch, int64_t seq_stride_rows,
+               int64_t capacity, int64_t row_bytes, const int64_t *lens,
+               hexkv_stream_t stream);
+
+/*
+ * Unpack: the mirror of hexkv_pack.  Rows [0, lens[b]) of every sequence of
+ * cache_layers[l] are overwritten from packed_layers[l]; every other cache row
+ * is left untouched.
+ *
+ * Replaces the per-layer cache rebuild of Engine.decode,
+ *   full = torch.empty((1, max_sequence_len, ...)); full[:, :L].copy_(live)
+ *   (hexgen2/model.py:104-108), writing into a cache the caller preallocated.
+ */
+int hexkv_unpack(const void *const *packed_layers, void *const *cache_layers,
+                 int n_layers, int batch, int64_t seq_stride_rows,
+                 int64_t capacity, int64_t row_bytes, const int64_t *lens,
+                 hexkv_stream_t stream);
+
+/*
+ * Append: for every sequence b < batch, copy row b of kv_new ([batch][row],
+ * contiguous) into the cache at position
+ *   pos_b = (positions_dev ? positions_dev[b] : 0) + position_bias.
+ * Rows with pos_b outside [0, capacity) are skipped on the device (the host
+ * wrapper rejects them first whenever positions are known on the host).
+ *
+ * Replaces the slice assignment of _update_kv_cache,
+ *   kv_cache[batch_start:batch_end, sequence_start:sequence_end, ...] = kv
+ *   (hexgen/hexgen_core/modules/mha.py:286), with per-sequence positions in
+ *   place of the single sequence_len_offset (mha.py:276-279).
+ *
+ *   cache             device base of [batch..][capacity][row] (the caller
+ *                     adds batch_size_offset * seq_stride_rows * row_bytes)
+ *   positions_dev     device int32 [batch] or NULL
+ */
+int hexkv_append(const void *kv_new, void *cache, int batch,
+                 int64_t seq_stride_rows, int64_t capacity, int64_t row_bytes,
+                 const int32_t *positions_dev, int32_t position_bias,
+                 hexkv_stream_t stream);
+
+/*
+ * Geometry and inputs of one attention call.  Strides are in elements.
+ * Query row r = (b, t), b < batch, t < q_len; q and out are
+ * [batch][q_len][q_heads][head_dim] with the two innermost dims contiguous.
+ * The cache is one layer: K of position s, head h at
+ *   cache + b*cache_batch_stride + s*cache_pos_stride + h*head_dim
+ * and V at that address + cache_kv_stride.
+ */
+typedef struct hexkv_attend_params {
+  int dtype;      /* enum hexkv_dtype, shared by q, cache, kv_new, out    */
+  int batch;      /* B                                                    */
+  int q_len;      /* queries per sequence (1 for decode)                  */
+  int q_heads;    /* Hq                                                   */
+  int kv_heads;   /* Hkv, divides Hq                                      */
+  int head_dim;   /* D: 16, 32, 64, 128 or 256                            */
+  int causal;     /* q_len > 1 only: query t sees keys < len - q_len + t + 1 */
+  float softmax_scale;
+  const void *q;
+  int64_t q_batch_stride, q_row_stride;
+  const void *cache;
+  int64_t cache_batch_stride, cache_pos_stride, cache_kv_stride;
+  int64_t capacity; /* positions per sequence in the cache */
+  void *out;
+  int64_t out_batch_stride, out_row_stride;
+  /* Keys attended by sequence b: len_b = (seqlens_dev ? seqlens_dev[b] : 0)
+   * + seqlen_bias, plus one when kv_new is set.  max_seqlen bounds every
+   * len_b (including that +1) and sizes the grid. */
+  const int32_t *seqlens_dev;
+  int32_t seqlen_bias;
+  int32_t max_seqlen;
+  /* Optional fused append (q_len == 1 only): kv_new is [batch][2][kv_heads]
+   * [head_dim] contiguous; its row is written to cache position len_b - 1 and
+   * attended from registers. */
+  const void *kv_new;
+  /* Split-K partition size in positions; 0 = chosen by the library. */
+  int partition;
+} hexkv_attend_params;
+
+/* Workspace bytes hexkv_attend needs for these parameters (0 when one
+ * partition covers every sequence). */
+size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p);
+
+/*
+ * Single-query GQA attention over the cache, optionally appending first:
+ *   out[b,t,h] = sum_s softmax_s(q[b,t,h] . K[b,s,h/g] * scale) V[b,s,h/g]
+ * over s < len(b,t), g = q_heads / kv_heads, fp32 accumulation.
+ *
+ * Replaces the decode-time attention of MHA.forward,
+ *   context = self.inner_cross_attn(q, kv, causal=False)
+ *   (hexgen/hexgen_core/modules/mha.py:568-569) -> FlashCrossAttention.forward
+ *   (mha.py:105-142), whose CPU semantics are CrossAttention.forward
+ *   (mha.py:209-244, GQA head repeat mha.py:223-224).  With kv_new set it also
+ *   replaces the preceding _update_kv_cache call (mha.py:565, 286).
+ */
+int hexkv_attend(const hexkv_attend_params *p, void *workspace,
+                 size_t workspace_bytes, hexkv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HEXKV_H_ */

@@ -1,0 +1,159 @@
+"""CPU oracle of the KV-cache data path -- TEST INFRASTRUCTURE ONLY.
+
+A plain numpy restatement of what the reference computes on this path.  Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
+may import it, and only as the checker: the product path (``hexgen2_amd``)
+never calls it and has no CPU fallback.
+
+Functions and the reference code each one restates:
+
+* ``pack``      hexgen2/model.py:78-81   live prefix of each layer's cache,
+                                         generalised to ragged batches; layers
+                                         concatenated in send order
+                                         (hexgen2/transport.py:56-59)
+* ``unpack``    hexgen2/model.py:101-108 scatter into a preallocated cache
+* ``append``    hexgen/hexgen_core/modules/mha.py:276-288 (slice assignment,
+                                         per-sequence offsets)
+* ``attend``    hexgen/hexgen_core/modules/mha.py:209-244 (CrossAttention:
+                                         GQA repeat :223-224, scale :231,
+                                         causal mask :238-241, softmax :242)
+                                         evaluated in float64
+* ``packet_payload_bytes``  hexgen2/transport.py:37 (payload accounting)
+
+Pinning (tests/test_oracle.py): pack/unpack/append against element-by-element
+Python loops on small inputs, the round-trip and untouched-row invariants, and
+the reference's recorded handoff byte counts (evidence/2026-10-19/
+fabric-pilot.json); attend against closed forms (one key -> that value, equal
+keys -> mean of values, a dominant key -> its value, group 1 == MHA), a
+scalar-loop restatement on small shapes, and torch's
+scaled_dot_product_attention in float64.
+"""
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import numpy as np
+
+
+def cu_lengths(lens: Sequence[int]) -> np.ndarray:
+    """Prefix sums [0, L0, L0+L1, ...]: packed row offset of each sequence."""
+    out = np.zeros(len(lens) + 1, dtype=np.int64)
+    np.cumsum(np.asarray(lens, dtype=np.int64), out=out[1:])
+    return out
+
+
+def pack(caches: Sequence[np.ndarray], lens: Sequence[int]) -> np.ndarray:
+    """caches: per layer [B, S, *row]; returns [n_layers, sum(lens), *row].
+
+    Row ``cu[b] + s`` of layer l is ``caches[l][b, s]`` for s < lens[b].
+    """
+    layers = []
+    for cache in caches:
+        if len(lens) != cache.shape[0]:
+            raise ValueError("one length per sequence")
+        if any(n < 0 or n > cache.shape[1] for n in lens):
+            raise ValueError("length outside [0, capacity]")
+        # model.py:81 -- t[:, :L] per sequence, concatenated in batch order
+        layers.append(np.concatenate([cache[b, :n] for b, n in enumerate(lens)], axis=0))
+    return np.stack(layers, axis=0)
+
+
+def unpack(packed: np.ndarray, caches: Sequence[np.ndarray], lens: Sequence[int]) -> list:
+    """Returns copies of ``caches`` with rows [0, lens[b]) of every sequence
+    replaced from ``packed``; all other rows unchanged."""
+    cu = cu_lengths(lens)
+    out = []
+    for l, cache in enumerate(caches):
+        cache = cache.copy()
+        for b, n in enumerate(lens):
+            # model.py:107 -- full[:, :L].copy_(live)
+            cache[b, :n] = packed[l, cu[b]:cu[b] + n]
+        out.append(cache)
+    return out
+
+
+def append(cache: np.ndarray, kv_new: np.ndarray, positions: Sequence[int]) -> np.ndarray:
+    """Copy of ``cache`` [B, S, *row] with ``cache[b, positions[b]] = kv_new[b]``."""
+    cache = cache.copy()
+    for b, pos in enumerate(positions):
+        if not 0 <= pos < cache.shape[1]:
+            # mha.py:282 asserts sequence_end <= capacity
+            raise ValueError("append position outside the cache")
+        cache[b, pos] = kv_new[b].reshape(cache.shape[2:])
+    return cache
+
+
+def attend(q: np.ndarray, cache: np.ndarray, lens: Sequence[int], causal: bool = False,
+           softmax_scale: float | None = None) -> np.ndarray:
+    """Float64 attention of q [B, Sq, Hq, D] over cache [B, S, 2, Hkv, D].
+
+    Sequence b attends keys [0, lens[b]); with ``causal`` query t of Sq sees
+    keys [0, lens[b] - Sq + t + 1) (equal to CrossAttention's triangular mask
+    when Sq == lens[b], the prefill case).  Returns [B, Sq, Hq, D] float64.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    cache = np.asarray(cache, dtype=np.float64)
+    batch, sq, hq, d = q.shape
+    hkv = cache.shape[3]
+    g = hq // hkv
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    out = np.zeros_like(q)
+    for b in range(batch):
+        n = int(lens[b])
+        # mha.py:223-224 -- repeat "... hkv d -> ... (hkv g) d": q head h uses kv head h // g
+        k = np.repeat(cache[b, :n, 0], g, axis=1)  # [n, Hq, D]
+        v = np.repeat(cache[b, :n, 1], g, axis=1)
+        scores = np.einsum("thd,shd->hts", q[b], k * scale)  # mha.py:231
+        if causal:
+            t_idx = np.arange(sq)[:, None]
+            s_idx = np.arange(n)[None, :]
+            scores = np.where(s_idx <= n - sq + t_idx, scores, -np.inf)
+        scores = scores - scores.max(axis=-1, keepdims=True)
+        p = np.exp(scores)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[b] = np.einsum("hts,shd->thd", p, v)  # mha.py:244
+    return out
+
+
+def attend_loop(q, cache, lens, softmax_scale=None) -> np.ndarray:
+    """Scalar-loop restatement of ``attend`` (non-causal) for tiny shapes."""
+    batch, sq, hq, d = q.shape
+    hkv = cache.shape[3]
+    g = hq // hkv
+    scale = 1.0 / math.sqrt(d) if softmax_scale is None else softmax_scale
+    out = np.zeros((batch, sq, hq, d))
+    for b in range(batch):
+        for t in range(sq):
+            for h in range(hq):
+                kvh = h // g
+                scores = []
+                for s in range(int(lens[b])):
+                    scores.append(sum(float(q[b, t, h, i]) * float(cache[b, s, 0, kvh, i])
+                                      for i in range(d)) * scale)
+                m = max(scores)
+                w = [math.exp(x - m) for x in scores]
+                z = sum(w)
+                for i in range(d):
+                    out[b, t, h, i] = sum(w[s] * float(cache[b, s, 1, kvh, i])
+                                          for s in range(len(w))) / z
+    return out
+
+
+DTYPE_BYTES = {"torch.float16": 2, "torch.bfloat16": 2, "torch.float32": 4,
+               "torch.float64": 8, "torch.int64": 8, "torch.int32": 4, "torch.int16": 2,
+               "torch.int8": 1, "torch.uint8": 1, "torch.bool": 1}
+
+
+def packet_payload_bytes(tensors: Sequence[tuple]) -> int:
+    """Sum of prod(shape) * element size over (shape, dtype-name) pairs
+    (transport.py:37)."""
+    return sum(math.prod(shape) * DTYPE_BYTES[dtype] for shape, dtype in tensors)
+
+
+def kv_packet_bytes(n_layers: int, prompt_len: int, kv_heads: int, head_dim: int,
+                    elem_bytes: int) -> int:
+    """Bytes of the pilot's KV packet: the int64 first token plus one
+    [1, L, 2, Hkv, D] live slice per layer (run.py:147-148)."""
+    row = 2 * kv_heads * head_dim * elem_bytes
+    return 8 + n_layers * prompt_len * row

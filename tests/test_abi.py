@@ -1,0 +1,92 @@
+"""The C-ABI boundary, checked without a GPU: the built library loads, exports
+every function include/hexkv.h declares, the ctypes mirror of
+``hexkv_attend_params`` has the C layout, and argument validation fails
+before any launch."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+from hexgen2_amd import _lib, ops
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hexkv.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(hexkv_[a-z_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.hexkv_version() >= 100
+    assert lib.hexkv_last_error() == b""
+
+
+def test_attend_params_layout_matches_c(tmp_path):
+    fields = [f[0] for f in _lib.AttendParams._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "hexkv.h"\nint main(void){\n'
+                   'printf("%zu\\n", sizeof(hexkv_attend_params));\n'
+                   + "".join(f'printf("%zu\\n", offsetof(hexkv_attend_params, {f}));\n' for f in fields)
+                   + "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)],
+                   check=True)
+    values = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert values[0] == ctypes.sizeof(_lib.AttendParams)
+    assert values[1:] == [getattr(_lib.AttendParams, f).offset for f in fields]
+
+
+def test_header_compiles_as_cxx(tmp_path):
+    src = tmp_path / "x.cpp"
+    src.write_text('#include "hexkv.h"\nint (*volatile probe)(void) = &hexkv_version;\nint main(){ return probe == nullptr; }\n')
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-c", f"-I{ROOT / 'include'}", str(src),
+                    "-o", str(tmp_path / "x.o")], check=True)
+
+
+def test_validation_fails_before_launch():
+    lib = _lib.load()
+    ptr = (ctypes.c_void_p * 1)(16)
+    lens = (ctypes.c_int64 * 1)(9)
+    # length above capacity -> HEXKV_ERANGE, nothing launched
+    assert lib.hexkv_pack(ptr, ptr, 1, 1, 8, 8, 512, lens, None) == _lib.HEXKV_ERANGE
+    assert b"outside" in lib.hexkv_last_error()
+    assert lib.hexkv_pack(ptr, ptr, 1, 1, 8, 8, 510, lens, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_append(None, None, 1, 8, 8, 512, None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_append(16, 16, 1, 8, 8, 512, None, 8, None) == _lib.HEXKV_ERANGE
+    p = _lib.AttendParams(dtype=1, batch=1, q_len=1, q_heads=4, kv_heads=2, head_dim=48, capacity=8, max_seqlen=4)
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_EUNSUPPORTED
+    p.head_dim, p.q_heads = 64, 3
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_EINVAL
+    p.q_heads, p.max_seqlen = 4, 9
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_ERANGE
+    # nothing to do is not an error
+    assert lib.hexkv_pack(ptr, ptr, 0, 1, 8, 8, 512, lens, None) == _lib.HEXKV_OK
+
+
+def test_status_codes_map_to_reference_exception_types():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.HEXKV_EINVAL, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.HEXKV_EUNSUPPORTED, "x")
+    with pytest.raises(_lib.HexKVError):
+        _lib.check(_lib.HEXKV_EHIP, "x")
+
+
+def test_cpu_tensors_are_rejected_loudly():
+    cache = torch.zeros((1, 4, 2, 1, 8))
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        ops.pack_live([cache], [2])
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        ops.decode_attention(torch.zeros((1, 1, 2, 8)), cache, max_seqlen=2, seqlen_bias=2)

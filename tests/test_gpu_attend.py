@@ -1,0 +1,165 @@
+"""GPU parity of decode attention (hexkv_attend) against the float64 oracle.
+
+Tolerances (max-abs, inputs rounded to the dtype first, oracle in float64):
+fp16 2e-3, bf16 8e-3, fp32 2e-5.  The fused append must also write the new
+row bit-exactly and touch nothing else.
+"""
+import numpy as np
+import pytest
+import torch
+
+from hexgen2_amd import ops
+from oracle import kv_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 8e-3, torch.float32: 2e-5}
+INT_VIEW = {torch.float16: torch.int16, torch.bfloat16: torch.int16, torch.float32: torch.int32}
+
+
+def bits(t):
+    return t.detach().cpu().contiguous().view(INT_VIEW[t.dtype]).numpy()
+
+
+def f64(t):
+    return t.detach().cpu().double().numpy()
+
+
+def make(batch, cap, hq, hkv, d, dtype, seed, device, q_len=1):
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn((batch, q_len, hq, d), generator=g, device=device).to(dtype)
+    cache = torch.randn((batch, cap, 2, hkv, d), generator=g, device=device).to(dtype)
+    return q, cache
+
+
+def check(out, q, cache, lens, dtype, causal=False, scale=None):
+    ref = oracle.attend(f64(q), f64(cache), lens, causal=causal, softmax_scale=scale)
+    err = np.abs(f64(out) - ref).max()
+    assert err <= TOL[dtype], f"max-abs error {err} > {TOL[dtype]}"
+    return err
+
+
+# (hq, hkv, d, dtype): the geometry of every configuration plus edge groups
+GEOMETRIES = [
+    (4, 4, 16, torch.float32),     # tiny llama, fp32
+    (4, 2, 32, torch.float16),     # reference fixture
+    (32, 4, 64, torch.float16),    # TinyLlama-1.1B
+    (32, 32, 128, torch.float16),  # Llama-2-7B
+    (8, 1, 128, torch.bfloat16),   # Llama-2-70B TP-8 share
+    (32, 8, 128, torch.bfloat16),  # Llama-3-8B
+    (32, 2, 128, torch.bfloat16),  # group 16 -> two head groups per KV head
+    (6, 2, 64, torch.float16),     # group 3 -> one head per workgroup
+    (4, 2, 256, torch.bfloat16),   # head_dim 256
+    (8, 8, 128, torch.float32),    # fp32, 32 lanes per position
+]
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", GEOMETRIES)
+def test_ragged_lengths_within_tolerance(device, hq, hkv, d, dtype):
+    lens = [1, 63, 64, 65, 700, 1500, 2049]
+    cap = 2112
+    print(f"attend hq={hq} hkv={hkv} d={d} {dtype} lens={lens}", flush=True)
+    q, cache = make(len(lens), cap, hq, hkv, d, dtype, 1, device)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    for partition in (0, 64, 512):
+        out = ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=partition)
+        torch.cuda.synchronize()
+        check(out, q, cache, lens, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_uniform_length_and_scale(device, dtype):
+    q, cache = make(3, 300, 16, 4, 128, dtype, 2, device)
+    out = ops.decode_attention(q, cache, max_seqlen=257, seqlen_bias=257, softmax_scale=0.05)
+    check(out, q, cache, [257] * 3, dtype, scale=0.05)
+
+
+def test_single_key_returns_value_exactly(device):
+    q, cache = make(2, 8, 8, 2, 64, torch.bfloat16, 3, device)
+    out = ops.decode_attention(q, cache, max_seqlen=1, seqlen_bias=1)
+    want = cache[:, 0, 1].repeat_interleave(4, dim=1)
+    assert torch.equal(out[:, 0], want)
+
+
+def test_dominant_key_selects_value(device):
+    q, cache = make(1, 40, 4, 4, 128, torch.float16, 4, device)
+    q.zero_()
+    q[0, 0, :, 0] = 1.0
+    cache[0, :, 0].zero_()
+    cache[0, 17, 0, :, 0] = 60.0
+    out = ops.decode_attention(q, cache, max_seqlen=40, seqlen_bias=40, softmax_scale=1.0)
+    torch.testing.assert_close(out[0, 0], cache[0, 17, 1], rtol=0, atol=1e-3)
+
+
+def test_zero_length_rows_give_zeros(device):
+    q, cache = make(3, 16, 8, 2, 64, torch.float16, 5, device)
+    lens = torch.tensor([0, 5, 0], dtype=torch.int32, device=device)
+    out = ops.decode_attention(q, cache, max_seqlen=5, seqlens=lens)
+    assert (out[0] == 0).all() and (out[2] == 0).all()
+    check(out[1:2], q[1:2], cache[1:2], [5], torch.float16)
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (32, 4, 64, torch.float16),
+                                           (4, 4, 16, torch.float32), (32, 2, 128, torch.bfloat16)])
+def test_fused_append_writes_row_and_attends_it(device, hq, hkv, d, dtype):
+    lens = [0, 5, 63, 64, 1023, 1024, 3000]
+    cap = 3100
+    q, cache = make(len(lens), cap, hq, hkv, d, dtype, 6, device)
+    g = torch.Generator(device=device).manual_seed(7)
+    kv_new = torch.randn((len(lens), 2, hkv, d), generator=g, device=device).to(dtype)
+    before = bits(cache)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    out = ops.decode_attention(q, cache, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new)
+    torch.cuda.synchronize()
+    want_cache = oracle.append(before, bits(kv_new), lens)
+    np.testing.assert_array_equal(bits(cache), want_cache)
+    check(out, q, cache, [n + 1 for n in lens], dtype)
+
+
+def test_fused_append_with_bias_matches_unfused(device):
+    q, cache = make(4, 200, 32, 8, 128, torch.bfloat16, 8, device)
+    kv_new = torch.randn((4, 2, 8, 128), device=device).to(torch.bfloat16)
+    base = torch.tensor([10, 0, 150, 98], dtype=torch.int32, device=device)
+    c1, c2 = cache.clone(), cache.clone()
+    o1 = ops.decode_attention(q, c1, max_seqlen=156, seqlens=base, seqlen_bias=5, kv_new=kv_new)
+    ops.append_kv(c2, kv_new.reshape(4, -1), base, position_bias=5)
+    o2 = ops.decode_attention(q, c2, max_seqlen=156, seqlens=base, seqlen_bias=6)
+    assert torch.equal(c1, c2)
+    assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_causal_prefill_rows(device, dtype):
+    q, cache = make(2, 40, 4, 2, 32, dtype, 9, device, q_len=7)
+    out = ops.decode_attention(q, cache, max_seqlen=40, seqlen_bias=7, causal=True)
+    check(out, q, cache, [7, 7], dtype, causal=True)
+    seqlens = torch.tensor([30, 7], dtype=torch.int32, device=device)
+    out = ops.decode_attention(q, cache, max_seqlen=40, seqlens=seqlens, causal=True)
+    check(out, q, cache, [30, 7], dtype, causal=True)
+
+
+def test_strided_cache_view_batch_offset(device):
+    # the view _update_kv_cache returns: cache[b0:b1, :offset+1]
+    q, cache = make(5, 64, 8, 2, 64, torch.float16, 10, device)
+    view = cache[1:4, :33]
+    out = ops.decode_attention(q[1:4], view, max_seqlen=33, seqlen_bias=33)
+    check(out, q[1:4], view, [33] * 3, torch.float16)
+
+
+def test_repeatable(device):
+    q, cache = make(8, 4096, 32, 8, 128, torch.bfloat16, 11, device)
+    lens = torch.randint(1, 4096, (8,), dtype=torch.int32, device=device)
+    a = ops.decode_attention(q, cache, max_seqlen=4096, seqlens=lens)
+    b = ops.decode_attention(q, cache, max_seqlen=4096, seqlens=lens)
+    assert torch.equal(a, b)
+
+
+def test_validation_errors(device):
+    q, cache = make(2, 16, 8, 2, 64, torch.float16, 12, device)
+    with pytest.raises(ValueError):
+        ops.decode_attention(q, cache, max_seqlen=17, seqlen_bias=17)  # beyond capacity
+    with pytest.raises(NotImplementedError):
+        qq, cc = make(1, 8, 2, 1, 48, torch.float16, 0, device)
+        ops.decode_attention(qq, cc, max_seqlen=4, seqlen_bias=4)  # head_dim 48 not compiled
+    with pytest.raises(ValueError):
+        ops.decode_attention(q.float(), cache, max_seqlen=4, seqlen_bias=4)  # dtype mismatch

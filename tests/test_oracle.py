@@ -1,0 +1,178 @@
+"""Pins the CPU oracle (oracle/kv_oracle.py) before it is trusted as the checker.
+
+Pack/unpack/append: element-by-element loops, the round-trip and untouched-row
+invariants, and the handoff sizes the reference recorded.  Attention: closed
+forms, a scalar-loop restatement, and torch's scaled_dot_product_attention in
+float64 as an independent library routine.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_oracle as oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _caches(rng, n_layers, batch, cap, hkv=2, d=3):
+    return [rng.standard_normal((batch, cap, 2, hkv, d)).astype(np.float32) for _ in range(n_layers)]
+
+
+@pytest.mark.parametrize("lens", [[4], [0, 3, 5], [5, 0, 0, 1], [1, 1, 1]])
+def test_pack_matches_elementwise_loop(lens):
+    rng = np.random.default_rng(0)
+    caches = _caches(rng, 3, len(lens), 5)
+    packed = oracle.pack(caches, lens)
+    assert packed.shape == (3, sum(lens), 2, 2, 3)
+    for l in range(3):
+        r = 0
+        for b, n in enumerate(lens):
+            for s in range(n):
+                for k in range(2):
+                    for h in range(2):
+                        for i in range(3):
+                            assert packed[l, r, k, h, i] == caches[l][b, s, k, h, i]
+                r += 1
+        assert r == sum(lens)
+
+
+def test_pack_batch1_equals_reference_slice():
+    # model.py:81: t[:, :L].contiguous() -- batch-1 packing is the plain slice
+    rng = np.random.default_rng(1)
+    caches = _caches(rng, 2, 1, 9)
+    packed = oracle.pack(caches, [6])
+    for l in range(2):
+        np.testing.assert_array_equal(packed[l], caches[l][0, :6])
+
+
+def test_unpack_roundtrip_and_untouched_rows():
+    rng = np.random.default_rng(2)
+    lens = [3, 0, 7, 1]
+    src = _caches(rng, 2, 4, 8)
+    packed = oracle.pack(src, lens)
+    sentinel = [np.full_like(c, -7.5) for c in src]
+    out = oracle.unpack(packed, sentinel, lens)
+    for l in range(2):
+        for b, n in enumerate(lens):
+            np.testing.assert_array_equal(out[l][b, :n], src[l][b, :n])
+            assert (out[l][b, n:] == -7.5).all()
+    # inputs are not modified
+    assert all((s == -7.5).all() for s in sentinel)
+
+
+def test_append_writes_exactly_one_row_per_sequence():
+    rng = np.random.default_rng(3)
+    cache = rng.standard_normal((3, 6, 2, 1, 4)).astype(np.float32)
+    kv = rng.standard_normal((3, 2, 1, 4)).astype(np.float32)
+    out = oracle.append(cache, kv, [0, 5, 2])
+    for b, pos in enumerate([0, 5, 2]):
+        np.testing.assert_array_equal(out[b, pos], kv[b])
+        for s in range(6):
+            if s != pos:
+                np.testing.assert_array_equal(out[b, s], cache[b, s])
+    with pytest.raises(ValueError):
+        oracle.append(cache, kv, [0, 6, 0])
+
+
+def test_packet_bytes_match_reference_evidence():
+    # kv_packet_bytes recorded by the reference pilot = int64 token + live KV
+    cases = json.loads((GOLDEN / "packet_bytes.json").read_text())["cases"]
+    assert len(cases) == 7
+    for c in cases:
+        assert oracle.kv_packet_bytes(c["layers"], c["prompt_tokens"], c["kv_heads"],
+                                      c["head_dim"], c["elem_bytes"]) == c["kv_packet_bytes"]
+        # and the same figure through the header payload accounting
+        shapes = [([1], "torch.int64")] + [([1, c["prompt_tokens"], 2, c["kv_heads"], c["head_dim"]],
+                                            "torch.float16")] * c["layers"]
+        assert oracle.packet_payload_bytes(shapes) == c["kv_packet_bytes"]
+    # pack output size agrees with the same accounting
+    c = cases[5]  # TinyLlama, 82-token prompt
+    caches = [np.zeros((1, 90, 2, 4, 64), np.float16)] * 2
+    assert oracle.pack(caches, [82]).nbytes == 2 * 82 * 1024
+
+
+def _rand_attn(rng, batch, sq, hq, hkv, d, cap):
+    q = rng.standard_normal((batch, sq, hq, d))
+    cache = rng.standard_normal((batch, cap, 2, hkv, d))
+    return q, cache
+
+
+def test_attend_single_key_returns_its_value():
+    rng = np.random.default_rng(4)
+    q, cache = _rand_attn(rng, 2, 1, 8, 2, 16, 4)
+    out = oracle.attend(q, cache, [1, 1])
+    for b in range(2):
+        for h in range(8):
+            np.testing.assert_allclose(out[b, 0, h], cache[b, 0, 1, h // 4], rtol=0, atol=1e-15)
+
+
+def test_attend_equal_keys_or_zero_query_average_values():
+    rng = np.random.default_rng(5)
+    q, cache = _rand_attn(rng, 1, 1, 4, 4, 8, 10)
+    cache[:, :, 0] = cache[:, :1, 0]  # every key equal
+    out = oracle.attend(q, cache, [7])
+    np.testing.assert_allclose(out[0, 0], cache[0, :7, 1].mean(axis=0), atol=1e-12)
+    q[:] = 0
+    q2, cache2 = _rand_attn(rng, 1, 1, 4, 4, 8, 10)
+    out = oracle.attend(np.zeros_like(q2), cache2, [10])
+    np.testing.assert_allclose(out[0, 0], cache2[0, :, 1].mean(axis=0), atol=1e-12)
+
+
+def test_attend_dominant_key_selects_its_value():
+    rng = np.random.default_rng(6)
+    q, cache = _rand_attn(rng, 1, 1, 2, 1, 16, 9)
+    cache[0, 5, 0, 0] = q[0, 0, 0] * 100.0  # huge score for q head 0 only
+    out = oracle.attend(q, cache, [9])
+    np.testing.assert_allclose(out[0, 0, 0], cache[0, 5, 1, 0], atol=1e-12)
+
+
+def test_attend_matches_scalar_loop_and_grouping():
+    rng = np.random.default_rng(7)
+    q, cache = _rand_attn(rng, 2, 1, 6, 2, 5, 7)
+    lens = [7, 3]
+    np.testing.assert_allclose(oracle.attend(q, cache, lens), oracle.attend_loop(q, cache, lens),
+                               rtol=1e-12, atol=1e-12)
+    # GQA with group g equals MHA over the head-repeated cache
+    mha_cache = np.repeat(cache, 3, axis=3)
+    np.testing.assert_allclose(oracle.attend(q, cache, lens), oracle.attend(q, mha_cache, lens),
+                               rtol=0, atol=1e-15)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attend_matches_torch_sdpa_fp64(causal):
+    rng = np.random.default_rng(8)
+    batch, sq, hq, hkv, d = 2, 5 if causal else 1, 8, 2, 32
+    lens = [5, 9] if causal else [13, 4]
+    q, cache = _rand_attn(rng, batch, sq, hq, hkv, d, 16)
+    out = oracle.attend(q, cache, lens, causal=causal, softmax_scale=0.3)
+    for b in range(batch):
+        n = lens[b]
+        k = torch.from_numpy(np.repeat(cache[b, :n, 0], hq // hkv, axis=1)).permute(1, 0, 2)
+        v = torch.from_numpy(np.repeat(cache[b, :n, 1], hq // hkv, axis=1)).permute(1, 0, 2)
+        qq = torch.from_numpy(q[b]).permute(1, 0, 2)
+        mask = None
+        if causal:  # bottom-right aligned triangle
+            mask = torch.arange(n)[None, :] <= (n - sq + torch.arange(sq))[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(qq, k, v, attn_mask=mask, scale=0.3)
+        np.testing.assert_allclose(out[b], ref.permute(1, 0, 2).numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_attend_causal_prefill_equals_reference_triangle():
+    # With Sq == Sk, query t sees keys <= t: CrossAttention's triu(-10000, 1) mask (mha.py:238-241)
+    rng = np.random.default_rng(9)
+    q, cache = _rand_attn(rng, 1, 6, 2, 2, 4, 6)
+    out = oracle.attend(q, cache, [6], causal=True)
+    for t in range(6):
+        row = oracle.attend(q[:, t:t + 1], cache, [t + 1])
+        np.testing.assert_allclose(out[:, t], row[:, 0], atol=1e-14)
+
+
+def test_attend_scale_default_is_inverse_sqrt_head_dim():
+    rng = np.random.default_rng(10)
+    q, cache = _rand_attn(rng, 1, 1, 2, 2, 16, 5)
+    np.testing.assert_allclose(oracle.attend(q, cache, [5]),
+                               oracle.attend(q, cache, [5], softmax_scale=1 / math.sqrt(16)), atol=0)

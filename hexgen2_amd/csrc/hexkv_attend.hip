@@ -51,6 +51,7 @@ struct AttendArgs {
   int32_t group;  // q heads per KV head
   int32_t part;   // positions per partition
   int32_t max_parts;
+  int32_t max_seqlen;  // host bound; every row length is clamped to it
   int64_t capacity;
   float scale_log2;  // softmax_scale * log2(e)
   float *ws_o;       // [rows][q_heads][max_parts][D]
@@ -67,7 +68,10 @@ __device__ __forceinline__ int row_length(const AttendArgs &a, int b, int t, int
     len += 1;
   }
   if (a.causal) len = len - a.q_len + t + 1;
-  if (len > a.capacity) len = static_cast<int>(a.capacity);
+  // Lengths come from device memory: clamp to the host bound that sized the
+  // grid and the workspace (max_seqlen <= capacity is checked on the host),
+  // so no row can reach past either.
+  if (len > a.max_seqlen) len = a.max_seqlen;
   return len;
 }
 
@@ -430,6 +434,7 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
   a.group = p->q_heads / p->kv_heads;
   a.part = part;
   a.max_parts = max_parts;
+  a.max_seqlen = p->max_seqlen;
   a.capacity = p->capacity;
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
   a.ws_o = static_cast<float *>(workspace);

@@ -24,6 +24,12 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Reinterpret one 32-bit lane word as a packed pair.  The word is taken by
+// value: applying __builtin_bit_cast directly to an ext-vector element
+// (v[i]) makes clang read element 0 whatever i is.
+__device__ __forceinline__ bf16x2 as_bf16x2(unsigned int w) { return __builtin_bit_cast(bf16x2, w); }
+__device__ __forceinline__ f16x2 as_f16x2(unsigned int w) { return __builtin_bit_cast(f16x2, w); }
+
 // ---------------------------------------------------------------- device ---
 
 // Sum over aligned groups of `LPP` consecutive lanes; every lane of a group
@@ -64,8 +70,7 @@ struct Elem<__bf16> {
   __device__ __forceinline__ static float dot(u32x4 a, u32x4 b, float acc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a[i]),
-                                            __builtin_bit_cast(bf16x2, b[i]), acc, false);
+      acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a[i]), as_bf16x2(b[i]), acc, false);
     return acc;
   }
   __device__ __forceinline__ static void to_float(u32x4 v, float *f) {
@@ -84,14 +89,13 @@ struct Elem<_Float16> {
   __device__ __forceinline__ static float dot(u32x4 a, u32x4 b, float acc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a[i]), __builtin_bit_cast(f16x2, b[i]),
-                                   acc, false);
+      acc = __builtin_amdgcn_fdot2(as_f16x2(a[i]), as_f16x2(b[i]), acc, false);
     return acc;
   }
   __device__ __forceinline__ static void to_float(u32x4 v, float *f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f16x2 h = __builtin_bit_cast(f16x2, v[i]);
+      const f16x2 h = as_f16x2(v[i]);
       f[2 * i] = static_cast<float>(h[0]);
       f[2 * i + 1] = static_cast<float>(h[1]);
     }

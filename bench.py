@@ -83,6 +83,32 @@ class Job:
             if ev is not None:
                 ev[3 + t].record()
 
+    def traffic_probe(self):
+        """A short fixed dispatch sequence for hardware-counter runs
+        (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE), in this order:
+
+        1. calibration: the pack kernel on one contiguous 2 GiB sequence, which
+           is a plain copy of exactly 2 GiB read + 2 GiB written;
+        2. pack of the workload; 3. unpack of the workload;
+        4. decode step 0 over every layer (fused append + attend).
+        """
+        w = self.w
+        rows = (2 << 30) // w.row_bytes
+        src = torch.ones((1, rows, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=self.q.device)
+        dst = torch.empty((1, rows, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=self.q.device)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {rows * w.row_bytes} bytes")
+        ops.pack_live([src], [rows], out=[dst[0]])
+        torch.cuda.synchronize()
+        del src, dst
+        log("pack, unpack, one decode step")
+        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
+        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        for l in range(w.layers):
+            self.plan(self.q[l], self.decode_layers[l], self.out, self.kv_new[l], 0, self.max_len + 1)
+        torch.cuda.synchronize()
+        log("probe done")
+
     def verify(self):
         """Size-independent self-check on the full workload: the unpacked live
         rows equal the prefill cache's (before any append) and the packed
@@ -142,6 +168,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the short dispatch sequence for hardware-counter runs")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the KV path here runs prefill and decode on one "
@@ -152,6 +180,9 @@ def main():
     log(f"workload {w.describe()}")
     job = Job(w, device)
     log("buffers ready")
+    if args.traffic_probe:
+        job.traffic_probe()
+        return
     if not args.no_verify:
         job.verify()
         log("full-size pack/unpack round trip verified")
@@ -183,9 +214,14 @@ def main():
     decode_gbs = w.decode_bytes() / (decode_total_ms * 1e-3) / 1e9
     launch_bytes = w.decode_bytes() / (w.layers * w.decode_steps)
     attend_us = decode_total_ms * 1e3 / (w.layers * w.decode_steps)
+    # HBM bytes per attention launch from the hardware-counter runs (measured
+    # at decode step 0), carried to the average launch by their ratio to the
+    # algorithmic bytes of that step.
     traffic = None
     if TRAFFIC_FILE.is_file():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get(w.name, {}).get("attend_bytes_per_launch")
+        ratio = json.loads(TRAFFIC_FILE.read_text()).get(w.name, {}).get("traffic_over_algorithmic")
+        if ratio:
+            traffic = int(ratio * launch_bytes)
     result = {
         "metric": METRIC,
         "value": round(pu_gbs, 1),

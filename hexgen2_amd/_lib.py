@@ -11,6 +11,7 @@ from pathlib import Path
 LIBRARY = Path(__file__).resolve().parent / "libhexkv.so"
 
 HEXKV_F16, HEXKV_BF16, HEXKV_F32 = 0, 1, 2
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2}
 HEXKV_OK = 0
 HEXKV_EINVAL, HEXKV_ERANGE, HEXKV_EHIP, HEXKV_EUNSUPPORTED, HEXKV_EWORKSPACE = -1, -2, -3, -4, -5
 MAX_LAYERS_PER_LAUNCH = 96
@@ -33,7 +34,7 @@ class AttendParams(ctypes.Structure):
         ("capacity", ctypes.c_int64),
         ("out", ctypes.c_void_p), ("out_batch_stride", ctypes.c_int64), ("out_row_stride", ctypes.c_int64),
         ("seqlens_dev", ctypes.c_void_p), ("seqlen_bias", ctypes.c_int32), ("max_seqlen", ctypes.c_int32),
-        ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int),
+        ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int), ("kernel", ctypes.c_int),
     ]
 
 

@@ -6,25 +6,41 @@
 //   `part` consecutive cache positions of one sequence for G query heads that
 //   share one KV head, so every K/V byte is read by exactly one workgroup.
 //   Ragged lengths only change how many partitions a row has; every
-//   partition but the last is full, so work per workgroup is uniform.
+//   partition but the last is full, so work per workgroup is uniform and
+//   small partitions keep the tail of the launch short.
 //
-// Inside a workgroup, per partition:
-//   1. scores: lanes are grouped LPP = D*elem/16 per position; each lane
-//      loads one 16-byte slice of a K row (coalesced: a group reads the whole
-//      D-wide row) and dots it with its slice of the G query vectors held in
-//      registers (v_dot2_f32_{bf16,f16} for 16-bit types).  The LPP partial
-//      sums are combined with DPP lane moves and the scaled score (log2
-//      domain) goes to LDS as scores[p][G];
-//   2. softmax: workgroup max per head, exp2 in place in LDS, sum per head;
-//   3. values: the same lane mapping loads V slices and accumulates
-//      p * V in fp32 registers (G x 8 accumulators per lane); lane groups and
-//      waves are then reduced through LDS.
-//   K/V go straight from HBM to VGPRs with nontemporal loads: each byte is
-//   consumed by exactly one lane, so staging them in LDS would add LDS traffic
-//   without any reuse.  LDS holds what is shared: the score tile.
-// A row with one partition writes its normalised output directly; otherwise
-// each partition writes (unnormalised o, max, sum) to the workspace and
-// `combine_kernel` merges them.
+// Two kernels stream a partition; both keep every load in flight without a
+// barrier, address K/V as a uniform (SGPR) base plus a 32-bit lane offset,
+// run an online softmax in the log2 domain whose running maximum moves
+// lazily (only when a score exceeds it by more than kRescaleSlack, so the
+// accumulator rescale is a rare wave-uniform branch), and accumulate
+// o += p * V in fp32 registers:
+//
+// attend_valu_kernel (any dtype, any group): positions are dealt to "lane
+//   groups" of LPP lanes; a lane group reads one position's K and V head
+//   slice (LPP x 16 bytes each) per load slot, U slots per iteration.  Scores
+//   are v_dot2_f32_{bf16,f16} (fp32: fma) of the lane's K slice with its
+//   slice of the G query vectors, summed over the LPP lanes by DPP moves.
+//
+// attend_mfma_kernel (16-bit, the GQA group on a matrix core): a wave takes
+//   tiles of 16 positions.  K is loaded in the A-operand layout of
+//   v_mfma_f32_16x16x32_{bf16,f16} (lane = position, 16-byte head slices) and
+//   the G query heads of the group are the B operand, so D/32 MFMAs give the
+//   16 x G score tile with no cross-lane reduction.  The probabilities go
+//   through a small per-wave LDS tile to the lanes that hold V (one position
+//   per LPP lanes, as above).  The matrix core works on 16 columns of which G
+//   are used; it is idle otherwise, and the VALU work per byte drops.
+//
+// With kv_new (fused append) the new row is the last position of the row: it
+// is never read from the cache; one wave attends it from kv_new after the
+// streaming loop, and the workgroup owning it writes it to the cache.
+//
+// A row with one partition writes its normalised output directly.  With
+// several, each partition stores (unnormalised o, max, sum) to the workspace
+// and `combine_kernel`, launched next on the same stream, merges them.  (A
+// last-arriver merge inside the attention kernel needs an agent-scope release
+// per workgroup, which on this part writes back the whole L2 of the XCD and
+// serialises: measured 2-20x slower than the second launch.)
 #include "hexkv_common.h"
 
 #include <algorithm>
@@ -33,6 +49,8 @@ namespace hexkv {
 
 constexpr int kAttThreads = 256;
 constexpr int kAttWaves = kAttThreads / 64;
+constexpr float kRescaleSlack = 8.f;  // log2 units
+constexpr float kNoScore = -1e30f;    // finite "minus infinity" of the running max
 
 struct AttendArgs {
   const void *q;
@@ -53,9 +71,9 @@ struct AttendArgs {
   int32_t max_parts;
   int32_t max_seqlen;  // host bound; every row length is clamped to it
   int64_t capacity;
-  float scale_log2;  // softmax_scale * log2(e)
-  float *ws_o;       // [rows][q_heads][max_parts][D]
-  float *ws_ml;      // [rows][q_heads][max_parts][2]
+  float scale_log2;    // softmax_scale * log2(e), > 0
+  float *ws_o;         // [rows][q_heads][max_parts][D]
+  float *ws_ml;        // [rows][q_heads][max_parts][2]
 };
 
 // Number of keys query row (b, t) attends to; *pos_new = cache position of the
@@ -75,224 +93,578 @@ __device__ __forceinline__ int row_length(const AttendArgs &a, int b, int t, int
   return len;
 }
 
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// What one workgroup does: query row (b, t), head group qh0.., KV head hk,
+// positions [p0, p0 + n) of which the first n_cache come from the cache and,
+// when has_new, the last one (pos_new) from kv_new.
+struct Work {
+  int row, b, t, len, part, p0, n, n_cache, nparts, qh0, hk, pos_new;
+  bool has_new, writer;
+};
+
+// Fills `w`; returns false when the workgroup has nothing to do (after
+// writing the defined zero output of an empty row).
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kAttThreads) void attend_kernel(const AttendArgs a) {
-  using E = Elem<T>;
-  constexpr int VEC = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte slice
-  constexpr int LPP = D / VEC;                           // lanes per position
-  static_assert(LPP >= 1 && LPP <= 64, "head_dim does not map onto a wave");
-  constexpr int PPW = 64 / LPP;          // positions per wave per load
-  constexpr int PPI = PPW * kAttWaves;   // positions per workgroup per load
-  constexpr int U = 4;                   // loads in flight per lane
-  extern __shared__ float smem[];        // scores [part][G]; later [waves][G][D]
-  __shared__ float s_red[kAttWaves][G];
-  __shared__ float s_m[G], s_l[G];
-
-  const int row = blockIdx.z;
-  const int b = row / a.q_len, t = row - b * a.q_len;
-  int pos_new;
-  const int len = row_length(a, b, t, &pos_new);
-  const int part = blockIdx.x;
-  const int p0 = part * a.part;
-  const int qh0 = blockIdx.y * G;
-  T *out_row = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + qh0 * D;
-  if (len <= 0) {  // nothing to attend to: defined zero output
-    if (part == 0)
-      for (int i = threadIdx.x; i < G * D; i += kAttThreads) out_row[i] = E::from_float(0.f);
-    return;
-  }
-  if (p0 >= len) return;
-  const int n = min(a.part, len - p0);
-  const int nparts = (len + a.part - 1) / a.part;
-  const int hk = qh0 / a.group;
-
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int sub = lane % LPP, grp = lane / LPP;
-  const int slot = w * PPW + grp;  // position of this lane within a PPI tile
-
-  const T *qrow = static_cast<const T *>(a.q) + b * a.q_bs + t * a.q_rs + qh0 * D + sub * VEC;
-  u32x4 qv[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const u32x4 *>(qrow + g * D);
-
-  T *kbase = const_cast<T *>(static_cast<const T *>(a.cache)) + b * a.c_bs + hk * D + sub * VEC;
-  T *vbase = kbase + a.c_kv;
-  const T *knew = a.kv_new
-      ? static_cast<const T *>(a.kv_new) + (static_cast<int64_t>(b) * 2 * a.kv_heads + hk) * D + sub * VEC
-      : nullptr;
-  const T *vnew = knew ? knew + a.kv_heads * D : nullptr;
-  // The fused-append row is read from kv_new (never from the cache) and
-  // written to the cache by the lanes that load it; K by phase 1, V by
-  // phase 3, of the one workgroup per (row, head group) owning position
-  // pos_new.  Head groups sharing a KV head (G < group) all hold the same
-  // bytes; only the first writes.
-  const bool writer = (qh0 % a.group) == 0;
-
-  // ---- phase 1: scores -----------------------------------------------------
-  float mx[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) mx[g] = -INFINITY;
-  for (int i0 = 0; i0 < n; i0 += PPI * U) {
-    u32x4 kr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = i0 + u * PPI + slot;
-      const int s = p0 + p;
-      kr[u] = u32x4{0u, 0u, 0u, 0u};
-      if (p < n) {
-        if (s == pos_new) kr[u] = *reinterpret_cast<const u32x4 *>(knew);
-        else kr[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(kbase + s * a.c_ps));
-      }
+__device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
+  w.row = blockIdx.z;
+  w.b = w.row / a.q_len;
+  w.t = w.row - w.b * a.q_len;
+  w.len = row_length(a, w.b, w.t, &w.pos_new);
+  w.part = blockIdx.x;
+  w.p0 = w.part * a.part;
+  w.qh0 = blockIdx.y * G;
+  if (w.len <= 0) {
+    if (w.part == 0) {
+      T *out_row = static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D;
+      for (int i = threadIdx.x; i < G * D; i += kAttThreads) out_row[i] = Elem<T>::from_float(0.f);
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = i0 + u * PPI + slot;
-      float sc[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) sc[g] = group_sum<LPP>(E::dot(qv[g], kr[u], 0.f)) * a.scale_log2;
-      if (p < n) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) mx[g] = fmaxf(mx[g], sc[g]);
-        if (sub == 0) {
-#pragma unroll
-          for (int g = 0; g < G; ++g) smem[p * G + g] = sc[g];
-        }
-        if (p0 + p == pos_new && writer)
-          *reinterpret_cast<u32x4 *>(kbase + static_cast<int64_t>(pos_new) * a.c_ps) = kr[u];
-      }
-    }
+    return false;
   }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m = wave_max(mx[g]);
-    if (lane == 0) s_red[w][g] = m;
-  }
-  __syncthreads();
-  if (tid < G) {
-    float m = s_red[0][tid];
-#pragma unroll
-    for (int i = 1; i < kAttWaves; ++i) m = fmaxf(m, s_red[i][tid]);
-    s_m[tid] = m;
-  }
-  __syncthreads();
+  if (w.p0 >= w.len) return false;
+  w.n = min(a.part, w.len - w.p0);
+  w.nparts = (w.len + a.part - 1) / a.part;
+  w.hk = w.qh0 / a.group;
+  // The new row, when attended at all, is the row's last position.
+  w.has_new = a.kv_new != nullptr && w.pos_new == w.p0 + w.n - 1;
+  w.n_cache = w.n - (w.has_new ? 1 : 0);
+  // Head groups sharing a KV head (G < group) hold the same new row; only
+  // the first writes it.
+  w.writer = w.has_new && (w.qh0 % a.group) == 0;
+  return true;
+}
 
-  // ---- phase 2: exponentiate in place, sum per head -----------------------
-  {
-    const int g = tid % G;  // G divides 256: a thread always sees one head
-    const float m = s_m[g];
-    float l = 0.f;
-    for (int i = tid; i < n * G; i += kAttThreads) {
-      const float e = exp2f(smem[i] - m);
-      smem[i] = e;
-      l += e;
-    }
-#pragma unroll
-    for (int off = 32; off >= G; off >>= 1) l += __shfl_xor(l, off);
-    if (lane < G) s_red[w][lane] = l;
-  }
-  __syncthreads();
-  if (tid < G) {
-    float l = 0.f;
-#pragma unroll
-    for (int i = 0; i < kAttWaves; ++i) l += s_red[i][tid];
-    s_l[tid] = l;
-  }
-  // (s_l is read only after the barrier that follows phase 3.)
-
-  // ---- phase 3: o = sum_p e_p * V_p ---------------------------------------
-  float acc[G][VEC];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[g][e] = 0.f;
-  for (int i0 = 0; i0 < n; i0 += PPI * U) {
-    u32x4 vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = i0 + u * PPI + slot;
-      const int s = p0 + p;
-      vr[u] = u32x4{0u, 0u, 0u, 0u};
-      if (p < n) {
-        if (s == pos_new) vr[u] = *reinterpret_cast<const u32x4 *>(vnew);
-        else vr[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vbase + s * a.c_ps));
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int p = i0 + u * PPI + slot;
-      if (p < n) {
-        float pr[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) pr[g] = smem[p * G + g];
-        float vf[VEC];
-        E::to_float(vr[u], vf);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pr[g], vf[e], acc[g][e]);
-        if (p0 + p == pos_new && writer)
-          *reinterpret_cast<u32x4 *>(vbase + static_cast<int64_t>(pos_new) * a.c_ps) = vr[u];
-      }
-    }
-  }
-  // Reduce over the PPW lane groups of each wave (lanes with equal `sub`).
-#pragma unroll
-  for (int off = LPP; off < 64; off <<= 1)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
-  __syncthreads();  // all score reads done: smem becomes [waves][G][D]
-  if (grp == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) smem[(w * G + g) * D + sub * VEC + e] = acc[g][e];
-  }
-  __syncthreads();
-  for (int i = tid; i < G * D; i += kAttThreads) {
-    float o = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < kAttWaves; ++ww) o += smem[ww * G * D + i];
+// Merges the 4 waves' (max, sum, o) held in LDS into this partition's result:
+// the normalised output for a single-partition row, else a workspace partial.
+template <typename T, int D, int G>
+__device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
+                                            const float (*s_acc)[G][D], const float (*s_m)[G],
+                                            const float (*s_l)[G]) {
+  T *out_row = static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D;
+  const int64_t slot0 = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0) * a.max_parts;
+  for (int i = threadIdx.x; i < G * D; i += kAttThreads) {
     const int g = i / D, d = i - g * D;
-    if (nparts == 1) {
-      out_row[i] = E::from_float(o / s_l[g]);
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int ww = 1; ww < kAttWaves; ++ww) mx = fmaxf(mx, s_m[ww][g]);
+    float o = 0.f, sum = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kAttWaves; ++ww) {
+      const float c = fast_exp2(s_m[ww][g] - mx);
+      o = fmaf(c, s_acc[ww][g][d], o);
+      sum = fmaf(c, s_l[ww][g], sum);
+    }
+    if (w.nparts == 1) {
+      out_row[i] = Elem<T>::from_float(o / sum);
     } else {
-      const int64_t slot_idx = (static_cast<int64_t>(row) * a.q_heads + qh0 + g) * a.max_parts + part;
-      a.ws_o[slot_idx * D + d] = o;
+      const int64_t slot = slot0 + static_cast<int64_t>(g) * a.max_parts + w.part;
+      a.ws_o[slot * D + d] = o;
       if (d == 0) {
-        a.ws_ml[slot_idx * 2] = s_m[g];
-        a.ws_ml[slot_idx * 2 + 1] = s_l[g];
+        a.ws_ml[slot * 2] = mx;
+        a.ws_ml[slot * 2 + 1] = sum;
       }
     }
   }
 }
 
-// Merges the partitions of one (query row, q head): o = sum_p w_p o_p / sum_p
-// w_p l_p with w_p = 2^(m_p - max m).
-template <typename T>
-__global__ __launch_bounds__(64) void combine_kernel(const AttendArgs a, int D) {
+__device__ __forceinline__ u32x4 load16(const char *base, uint32_t off) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + off));
+}
+
+// Lane geometry of one (dtype, head_dim) for reading a head row: each lane
+// owns EPL consecutive elements (NV 16-byte vectors), LPP lanes cover it.
+template <typename T, int D>
+struct Lanes {
+  static constexpr int VEC = 16 / static_cast<int>(sizeof(T));
+  static constexpr int NV = D / VEC > 16 ? D / (VEC * 16) : 1;
+  static constexpr int EPL = VEC * NV;
+  static constexpr int LPP = D / EPL;
+  static constexpr int GPW = 64 / LPP;
+  static constexpr int NG = GPW * kAttWaves;
+  static_assert(LPP >= 1 && LPP <= 16 && EPL * LPP == D, "head_dim does not map onto a wave");
+};
+
+// Running-softmax state update for one tile of scores: moves the running
+// maximum of head g to the tile maximum `mt[g]` (scaled) when it exceeds the
+// old one by more than kRescaleSlack, rescaling l and the accumulators.
+template <int G, int EPL>
+__device__ __forceinline__ void lazy_rescale(const float (&mt)[G], float (&m)[G], float (&l)[G],
+                                             float (&acc)[G][EPL]) {
+  bool grow = false;
+  float mnew[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const bool up = mt[g] > m[g] + kRescaleSlack;
+    mnew[g] = up ? mt[g] : m[g];
+    grow |= up;
+  }
+  if (__any(grow)) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float c = fast_exp2(m[g] - mnew[g]);
+      m[g] = mnew[g];
+      l[g] *= c;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] *= c;
+    }
+  }
+}
+
+// ------------------------------------------------------------- VALU path ---
+
+template <typename T, int D, int G, int U>
+__global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendArgs a) {
   using E = Elem<T>;
-  const int h = blockIdx.x, row = blockIdx.y;
+  using L = Lanes<T, D>;
+  constexpr int VEC = L::VEC, NV = L::NV, EPL = L::EPL, LPP = L::LPP, GPW = L::GPW, NG = L::NG;
+  constexpr int STEP = NG * U;  // positions per workgroup iteration
+  __shared__ float s_acc[kAttWaves][G][D];
+  __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
+  Work w;
+  if (!begin_work<T, D, G>(a, w)) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane % LPP, gid = wave * GPW + lane / LPP;
+  const float scale = a.scale_log2;
+
+  const T *qrow = static_cast<const T *>(a.q) + w.b * a.q_bs + w.t * a.q_rs + w.qh0 * D + sub * EPL;
+  u32x4 qv[G][NV];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) qv[g][v] = *reinterpret_cast<const u32x4 *>(qrow + g * D + v * VEC);
+
+  // Uniform bases of this sequence's K and V head slices; lane offsets are
+  // 32-bit (the host checks capacity * position stride fits).
+  const char *kseq = static_cast<const char *>(a.cache) +
+                     (w.b * a.c_bs + static_cast<int64_t>(w.hk) * D) * static_cast<int64_t>(sizeof(T));
+  const char *vseq = kseq + a.c_kv * static_cast<int64_t>(sizeof(T));
+  const uint32_t row_bytes = static_cast<uint32_t>(a.c_ps * sizeof(T));
+  const uint32_t lane_off = static_cast<uint32_t>(sub * EPL * sizeof(T));
+  const uint32_t lane_base = static_cast<uint32_t>(w.p0 + gid) * row_bytes + lane_off;
+
+  float m[G], l[G], acc[G][EPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNoScore;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+  }
+
+  // One iteration: U slots of one position per lane group.  TAIL clamps the
+  // positions past n_cache to the last cached one (finite data) and masks
+  // their scores.
+  auto step = [&](int i0, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
+    u32x4 kr[U][NV], vr[U][NV];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t off;
+      if constexpr (TAIL) {
+        const int p = min(i0 + u * NG + gid, w.n_cache - 1);
+        off = static_cast<uint32_t>(w.p0 + p) * row_bytes + lane_off;
+      } else {
+        off = lane_base + static_cast<uint32_t>(i0 + u * NG) * row_bytes;
+      }
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        kr[u][v] = load16(kseq, off + v * 16);
+        vr[u][v] = load16(vseq, off + v * 16);
+      }
+    }
+    float sc[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = E::dot(qv[g][0], kr[u][0], 0.f);
+#pragma unroll
+        for (int v = 1; v < NV; ++v) d = E::dot(qv[g][v], kr[u][v], d);
+        sc[u][g] = group_sum<LPP>(d);
+      }
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool valid = i0 + u * NG + gid < w.n_cache;
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[u][g] = valid ? sc[u][g] : -INFINITY;
+      }
+    }
+    float mt[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float x = sc[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) x = fmaxf(x, sc[u][g]);
+      mt[g] = x * scale;
+    }
+    lazy_rescale<G, EPL>(mt, m, l, acc);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vf[EPL];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) E::to_float(vr[u][v], vf + v * VEC);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = fast_exp2(fmaf(sc[u][g], scale, -m[g]));
+        l[g] += pr;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
+      }
+    }
+  };
+
+  int i0 = 0;
+  for (; i0 + STEP <= w.n_cache; i0 += STEP) step(i0, std::false_type{});
+  if (i0 < w.n_cache) step(i0, std::true_type{});
+
+  if (w.has_new) {
+    // The new row: attended by lane group 0 from kv_new, written to the cache
+    // by that lane group of the writer workgroup.
+    const char *knew = static_cast<const char *>(a.kv_new) +
+                       ((static_cast<int64_t>(w.b) * 2 * a.kv_heads + w.hk) * D) * static_cast<int64_t>(sizeof(T));
+    const char *vnew = knew + static_cast<int64_t>(a.kv_heads) * D * sizeof(T);
+    u32x4 kn[NV], vn[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      kn[v] = *reinterpret_cast<const u32x4 *>(knew + lane_off + v * 16);
+      vn[v] = *reinterpret_cast<const u32x4 *>(vnew + lane_off + v * 16);
+    }
+    float sc[G], mt[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = E::dot(qv[g][0], kn[0], 0.f);
+#pragma unroll
+      for (int v = 1; v < NV; ++v) d = E::dot(qv[g][v], kn[v], d);
+      sc[g] = gid == 0 ? group_sum<LPP>(d) : -INFINITY;
+      mt[g] = sc[g] * scale;
+    }
+    lazy_rescale<G, EPL>(mt, m, l, acc);
+    float vf[EPL];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) E::to_float(vn[v], vf + v * VEC);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float pr = fast_exp2(fmaf(sc[g], scale, -m[g]));
+      l[g] += pr;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
+    }
+    if (w.writer && gid == 0) {
+      const uint32_t off = static_cast<uint32_t>(w.pos_new) * row_bytes + lane_off;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(kseq) + off + v * 16) = kn[v];
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(vseq) + off + v * 16) = vn[v];
+      }
+    }
+  }
+
+  // Merge the GPW lane groups of this wave (lanes with equal `sub`).
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float mw = m[g];
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off));
+    const float c = fast_exp2(m[g] - mw);
+    m[g] = mw;
+    l[g] *= c;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] *= c;
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) {
+      l[g] += __shfl_xor(l[g], off);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+    }
+  }
+  if (lane < LPP) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) s_acc[wave][g][sub * EPL + e] = acc[g][e];
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  finish_work<T, D, G>(a, w, s_acc, s_m, s_l);
+}
+
+// ------------------------------------------------------------- MFMA path ---
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+};
+
+// Lane layouts of one wave and a 16-position tile:
+//   scores  lane l = (kg = l / 16, r = l % 16).  As the MFMA A operand lane l
+//           holds position r's 16-byte K slices 4j + kg (j < D/32, one per
+//           k-step); as the B operand it holds the same slices of query head
+//           r (zero for r >= G).  The result gives lane l the scores of
+//           positions 4 kg + e (e < 4) for head r.
+//   values  lane l = (vg = l / VLPP, vs = l % VLPP): position u VPPI + vg
+//           (u < UV), 16-byte slice vs, 8 elements per lane.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendArgs a) {
+  static_assert(sizeof(T) == 2 && G <= 16, "MFMA path: 16-bit types, up to 16 heads per group");
+  using E = Elem<T>;
+  constexpr int NJ = D / 32;       // k-steps of 32 elements
+  constexpr int VLPP = D / 8;      // value lanes per position
+  constexpr int VPPI = 64 / VLPP;  // positions per value load
+  constexpr int UV = 16 / VPPI;    // value loads per tile
+  static_assert(NJ >= 1 && VLPP <= 64 && UV >= 1 && UV * VPPI == 16, "head_dim");
+  __shared__ float s_p[kAttWaves][16][G];
+  __shared__ float s_acc[kAttWaves][G][D];
+  __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
+  Work w;
+  if (!begin_work<T, D, G>(a, w)) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kg = lane >> 4, r = lane & 15;
+  const int vg = lane / VLPP, vs = lane % VLPP;
+  const float scale = a.scale_log2;
+  const bool head_lane = r < G;
+
+  const T *qrow = static_cast<const T *>(a.q) + w.b * a.q_bs + w.t * a.q_rs + w.qh0 * D;
+  u32x4 qb[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    qb[j] = head_lane ? *reinterpret_cast<const u32x4 *>(qrow + r * D + (4 * j + kg) * 8) : u32x4{0u, 0u, 0u, 0u};
+
+  const char *kseq = static_cast<const char *>(a.cache) +
+                     (w.b * a.c_bs + static_cast<int64_t>(w.hk) * D) * static_cast<int64_t>(sizeof(T));
+  const char *vseq = kseq + a.c_kv * static_cast<int64_t>(sizeof(T));
+  const uint32_t row_bytes = static_cast<uint32_t>(a.c_ps * sizeof(T));
+  const uint32_t k_lane = static_cast<uint32_t>(w.p0 + r) * row_bytes + kg * 16;
+  const uint32_t v_lane = static_cast<uint32_t>(w.p0 + vg) * row_bytes + vs * 16;
+
+  // Score-layout state (lane r holds head r; m uniform over the 4 kg lanes).
+  float m = kNoScore, lp = 0.f;
+  // Value-layout accumulators.
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+
+  // One tile of 16 positions starting at p0 + i0 (kv_new for the new row).
+  auto tile = [&](int i0, auto mode) {
+    constexpr int MODE = decltype(mode)::value;  // 0 full, 1 tail, 2 new row
+    u32x4 kr[NJ], vr[UV];
+    if constexpr (MODE == 2) {
+      const char *knew = static_cast<const char *>(a.kv_new) +
+                         ((static_cast<int64_t>(w.b) * 2 * a.kv_heads + w.hk) * D) * static_cast<int64_t>(sizeof(T));
+      const char *vnew = knew + static_cast<int64_t>(a.kv_heads) * D * sizeof(T);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) kr[j] = *reinterpret_cast<const u32x4 *>(knew + (4 * j + kg) * 16);
+#pragma unroll
+      for (int u = 0; u < UV; ++u) vr[u] = *reinterpret_cast<const u32x4 *>(vnew + vs * 16);
+      if (w.writer && lane < VLPP) {
+        const uint32_t off = static_cast<uint32_t>(w.pos_new) * row_bytes + vs * 16;
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(kseq) + off) = *reinterpret_cast<const u32x4 *>(knew + vs * 16);
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(vseq) + off) = vr[0];
+      }
+    } else {
+      uint32_t koff, voff[UV];
+      if constexpr (MODE == 1) {
+        const int last = w.n_cache - 1;
+        koff = static_cast<uint32_t>(w.p0 + min(i0 + r, last)) * row_bytes + kg * 16;
+#pragma unroll
+        for (int u = 0; u < UV; ++u)
+          voff[u] = static_cast<uint32_t>(w.p0 + min(i0 + u * VPPI + vg, last)) * row_bytes + vs * 16;
+      } else {
+        koff = k_lane + static_cast<uint32_t>(i0) * row_bytes;
+#pragma unroll
+        for (int u = 0; u < UV; ++u) voff[u] = v_lane + static_cast<uint32_t>(i0 + u * VPPI) * row_bytes;
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) kr[j] = load16(kseq, koff + j * 64);
+#pragma unroll
+      for (int u = 0; u < UV; ++u) vr[u] = load16(vseq, voff[u]);
+    }
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) c = Mfma<T>::mma(kr[j], qb[j], c);
+    float s[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s[e] = c[e];
+      if constexpr (MODE == 1) s[e] = i0 + 4 * kg + e < w.n_cache ? s[e] : -INFINITY;
+      if constexpr (MODE == 2) s[e] = (kg == 0 && e == 0) ? s[e] : -INFINITY;
+    }
+    float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt *= scale;
+    const bool up = head_lane && mt > m + kRescaleSlack;
+    if (__any(up)) {
+      const float mnew = up ? mt : m;
+      const float cf = fast_exp2(m - mnew);
+      m = mnew;
+      lp *= cf;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float cg = readlane_f(cf, g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] *= cg;
+      }
+    }
+    float p[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[e] = fast_exp2(fmaf(s[e], scale, -m));
+      lp += p[e];
+    }
+    if (head_lane) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s_p[wave][4 * kg + e][r] = p[e];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < UV; ++u) {
+      const float *pp = s_p[wave][u * VPPI + vg];
+      float pg[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) pg[g] = pp[g];
+      float vf[8];
+      E::to_float(vr[u], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // Tiles of 16 positions, dealt round-robin to the waves.
+  const int full_tiles = w.n_cache / 16;
+  int ti = wave;
+  for (; ti < full_tiles; ti += kAttWaves) tile(ti * 16, std::integral_constant<int, 0>{});
+  if (ti * 16 < w.n_cache) tile(ti * 16, std::integral_constant<int, 1>{});
+  if (w.has_new && wave == 0) tile(0, std::integral_constant<int, 2>{});
+
+  // Wave totals: l over the 4 kg lanes of each head, o over the value lanes
+  // of each slice.
+  lp += __shfl_xor(lp, 16);
+  lp += __shfl_xor(lp, 32);
+#pragma unroll
+  for (int off = VLPP; off < 64; off <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+  if (lane < VLPP) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[wave][g][vs * 8 + e] = acc[g][e];
+  }
+  if (lane < G) {
+    s_m[wave][lane] = m;
+    s_l[wave][lane] = lp;
+  }
+  __syncthreads();
+  finish_work<T, D, G>(a, w, s_acc, s_m, s_l);
+}
+
+// Merges the partitions of one (query row, head group) of a split row:
+// o = sum_p w_p o_p with w_p = 2^(m_p - max m) / sum_p 2^(m_p - max m) l_p.
+// TPH lanes per head reduce (max, sum) over the partitions and stage the
+// weights in LDS; then each thread merges its outputs with all partition
+// loads of a chunk issued before they are used.
+constexpr int kCombineChunk = 256;  // partitions whose weights sit in LDS at once
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a) {
+  using E = Elem<T>;
+  constexpr int TPH = 256 / G < 64 ? 256 / G : 64;  // threads per head in the reduction
+  constexpr int PER = (G * D + kAttThreads - 1) / kAttThreads;  // outputs per thread
+  __shared__ float s_w[G][kCombineChunk];
+  __shared__ float s_mx[G], s_inv[G];
+  const int row = blockIdx.y, qh0 = blockIdx.x * G;
   const int b = row / a.q_len, t = row - b * a.q_len;
   int pos_new;
   const int len = row_length(a, b, t, &pos_new);
   if (len <= 0) return;
   const int nparts = (len + a.part - 1) / a.part;
   if (nparts <= 1) return;
-  const int64_t base = (static_cast<int64_t>(row) * a.q_heads + h) * a.max_parts;
-  const float *ml = a.ws_ml + base * 2;
-  float m = -INFINITY;
-  for (int p = 0; p < nparts; ++p) m = fmaxf(m, ml[2 * p]);
-  float l = 0.f;
-  for (int p = 0; p < nparts; ++p) l += exp2f(ml[2 * p] - m) * ml[2 * p + 1];
-  const float inv = 1.f / l;
-  T *out = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + static_cast<int64_t>(h) * D;
-  const float *o = a.ws_o + base * D;
-  for (int d = threadIdx.x; d < D; d += 64) {
-    float acc = 0.f;
-    for (int p = 0; p < nparts; ++p) acc += exp2f(ml[2 * p] - m) * o[p * D + d];
-    out[d] = E::from_float(acc * inv);
+  const int tid = threadIdx.x;
+  const int64_t slot0 = (static_cast<int64_t>(row) * a.q_heads + qh0) * a.max_parts;
+  const int hg = tid / TPH, hj = tid % TPH;
+  if (hg < G) {
+    const float *ml = a.ws_ml + (slot0 + static_cast<int64_t>(hg) * a.max_parts) * 2;
+    float mx = kNoScore;
+    for (int p = hj; p < nparts; p += TPH) mx = fmaxf(mx, ml[2 * p]);
+#pragma unroll
+    for (int off = TPH / 2; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float sum = 0.f;
+    for (int p = hj; p < nparts; p += TPH) sum = fmaf(fast_exp2(ml[2 * p] - mx), ml[2 * p + 1], sum);
+#pragma unroll
+    for (int off = TPH / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    if (hj == 0) {
+      s_mx[hg] = mx;
+      s_inv[hg] = 1.f / sum;
+    }
+  }
+  float acc[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) acc[k] = 0.f;
+  for (int c0 = 0; c0 < nparts; c0 += kCombineChunk) {
+    const int nc = min(kCombineChunk, nparts - c0);
+    __syncthreads();  // s_mx/s_inv ready; previous chunk's weights consumed
+    if (hg < G) {
+      const float *ml = a.ws_ml + (slot0 + static_cast<int64_t>(hg) * a.max_parts + c0) * 2;
+      for (int p = hj; p < nc; p += TPH) s_w[hg][p] = fast_exp2(ml[2 * p] - s_mx[hg]) * s_inv[hg];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + k * kAttThreads;
+      if (i < G * D) {
+        const int g = i / D, d = i - g * D;
+        const float *o = a.ws_o + (slot0 + static_cast<int64_t>(g) * a.max_parts + c0) * D + d;
+        int p = 0;
+        for (; p + 8 <= nc; p += 8) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = o[static_cast<int64_t>(p + u) * D];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) acc[k] = fmaf(s_w[g][p + u], v[u], acc[k]);
+        }
+        for (; p < nc; ++p) acc[k] = fmaf(s_w[g][p], o[static_cast<int64_t>(p) * D], acc[k]);
+      }
+    }
+  }
+  T *out_row = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + qh0 * D;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = tid + k * kAttThreads;
+    if (i < G * D) out_row[i] = E::from_float(acc[k]);
   }
 }
 
@@ -307,20 +679,31 @@ static int kernel_group(int group) {
   return 1;
 }
 
+// Partition size: about (rows x head groups x positions) / 2048 positions,
+// as a power of two in [64, 1024], counting half of max_seqlen per row
+// (ragged batches average about that).  Measured on MI355X: Llama-3-8B's
+// shape (64 rows x 8 groups, lengths to 8K) is fastest at 1024, Llama-2-7B's
+// (8 x 32, to 2K) at 128-512, the Llama-2-70B TP-8 share (32 x 1, to 4K) at
+// 128-256 and TinyLlama (1 x 4, 512) at 64.
 static int choose_partition(const hexkv_attend_params *p) {
   if (p->partition > 0) return p->partition;
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
   const int64_t groups = p->q_heads / kernel_group(p->q_heads / p->kv_heads);
-  const int64_t target = 1024;  // >= 4 workgroups per CU on a 256-CU part
-  for (int part = 1024; part >= 64; part >>= 1) {
-    const int64_t parts = (p->max_seqlen + part - 1) / part;
-    if (rows * groups * parts >= target) return part;
-  }
-  return 64;
+  const int64_t half = std::max<int64_t>(1, (p->max_seqlen + 1) / 2);
+  const int64_t want = rows * groups * half / 2048;
+  int part = 64;
+  while (part < 1024 && part < want) part <<= 1;
+  return part;
 }
 
+static int64_t max_parts_of(const hexkv_attend_params *p, int part) {
+  return std::max<int64_t>(1, (p->max_seqlen + part - 1) / part);
+}
+
+// Workspace: the partial outputs [rows][q_heads][max_parts][D], then their
+// (max, sum) pairs [rows][q_heads][max_parts][2], all fp32.
 static size_t workspace_bytes(const hexkv_attend_params *p, int part) {
-  const int64_t max_parts = (p->max_seqlen + part - 1) / part;
+  const int64_t max_parts = max_parts_of(p, part);
   if (max_parts <= 1) return 0;
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
   return static_cast<size_t>(rows * p->q_heads * max_parts * (p->head_dim + 2)) * sizeof(float);
@@ -346,6 +729,12 @@ static int validate(const hexkv_attend_params *p) {
                 p->max_seqlen, static_cast<long long>(p->capacity));
   if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > 4096)))
     return fail(HEXKV_EINVAL, "hexkv_attend: partition must be 0 or a multiple of 64 up to 4096");
+  if (!(p->softmax_scale > 0.f) || p->softmax_scale > 3.0e38f)
+    return fail(HEXKV_EINVAL, "hexkv_attend: softmax_scale must be positive and finite");
+  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_MFMA)
+    return fail(HEXKV_EINVAL, "hexkv_attend: unknown kernel %d", p->kernel);
+  if (p->kernel == HEXKV_KERNEL_MFMA && (p->dtype == HEXKV_F32 || p->head_dim < 64))
+    return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the MFMA kernel takes float16/bfloat16 with head_dim >= 64");
   if (p->batch == 0) return HEXKV_OK;
   if (!p->q || !p->cache || !p->out) return fail(HEXKV_EINVAL, "hexkv_attend: null tensor");
   const int vec = 16 / elem_size(p->dtype);
@@ -356,34 +745,64 @@ static int validate(const hexkv_attend_params *p) {
     return fail(HEXKV_EINVAL, "hexkv_attend: strides must be multiples of 16 bytes");
   if ((reinterpret_cast<uintptr_t>(p->out) & (elem_size(p->dtype) - 1)) != 0)
     return fail(HEXKV_EINVAL, "hexkv_attend: out misaligned");
+  // K/V are addressed as a per-sequence base plus a 32-bit byte offset.
+  if (p->cache_pos_stride <= 0 || p->cache_kv_stride < 0 ||
+      (static_cast<int64_t>(p->max_seqlen) * p->cache_pos_stride + p->cache_kv_stride +
+       static_cast<int64_t>(p->kv_heads) * d) * elem_size(p->dtype) > INT64_C(0xffffffff))
+    return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: one sequence of the cache spans more than 4 GiB");
   return HEXKV_OK;
 }
 
+// Load slots per lane group and iteration of the VALU kernel.  One slot
+// keeps the registers low enough for more resident waves, which measured
+// faster than 2 or 4 slots per wave at the partition sizes chosen above.
 template <typename T, int D, int G>
-static void launch(const AttendArgs &a, dim3 grid, size_t smem, hipStream_t s) {
-  attend_kernel<T, D, G><<<grid, kAttThreads, smem, s>>>(a);
+constexpr int slots() {
+  return 1;
+}
+
+// Kernel choice: the MFMA kernel for 16-bit data with head_dim >= 64 and 8+
+// query heads per KV head, where the matrix core takes enough of the group's
+// dot products to beat the VALU kernel (Llama-2-70B TP-8 share: 28.5 vs
+// 30.6 us; TinyLlama: 10.2 vs 10.8 us); the VALU kernel otherwise (Llama-3-8B,
+// group 4: 172.6 vs 181.7 us).
+static bool use_mfma(const hexkv_attend_params *p, int G) {
+  if (p->kernel == HEXKV_KERNEL_MFMA) return true;
+  if (p->kernel == HEXKV_KERNEL_VALU) return false;
+  return p->dtype != HEXKV_F32 && p->head_dim >= 64 && G >= 8;
+}
+
+template <typename T, int D, int G>
+static void launch(const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
+  if constexpr (sizeof(T) == 2 && D >= 64) {
+    if (mfma) attend_mfma_kernel<T, D, G><<<grid, kAttThreads, 0, s>>>(a);
+    else attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
+  } else {
+    attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
+  }
+  if (a.max_parts > 1) combine_kernel<T, D, G><<<dim3(grid.y, grid.z), kAttThreads, 0, s>>>(a);
 }
 
 template <typename T, int D>
-static int dispatch_g(int G, const AttendArgs &a, dim3 grid, size_t smem, hipStream_t s) {
+static int dispatch_g(int G, const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
   switch (G) {
-    case 1: launch<T, D, 1>(a, grid, smem, s); break;
-    case 2: launch<T, D, 2>(a, grid, smem, s); break;
-    case 4: launch<T, D, 4>(a, grid, smem, s); break;
-    case 8: launch<T, D, 8>(a, grid, smem, s); break;
+    case 1: launch<T, D, 1>(a, grid, mfma, s); break;
+    case 2: launch<T, D, 2>(a, grid, mfma, s); break;
+    case 4: launch<T, D, 4>(a, grid, mfma, s); break;
+    case 8: launch<T, D, 8>(a, grid, mfma, s); break;
     default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: group %d", G);
   }
   return HEXKV_OK;
 }
 
 template <typename T>
-static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, size_t smem, hipStream_t s) {
+static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
   switch (D) {
-    case 16: return dispatch_g<T, 16>(G, a, grid, smem, s);
-    case 32: return dispatch_g<T, 32>(G, a, grid, smem, s);
-    case 64: return dispatch_g<T, 64>(G, a, grid, smem, s);
-    case 128: return dispatch_g<T, 128>(G, a, grid, smem, s);
-    case 256: return dispatch_g<T, 256>(G, a, grid, smem, s);
+    case 16: return dispatch_g<T, 16>(G, a, grid, mfma, s);
+    case 32: return dispatch_g<T, 32>(G, a, grid, mfma, s);
+    case 64: return dispatch_g<T, 64>(G, a, grid, mfma, s);
+    case 128: return dispatch_g<T, 128>(G, a, grid, mfma, s);
+    case 256: return dispatch_g<T, 256>(G, a, grid, mfma, s);
     default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: head_dim %d", D);
   }
 }
@@ -392,7 +811,9 @@ static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, size_t smem,
 
 extern "C" size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p) {
   using namespace hexkv;
-  if (!p || p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads) return 0;
+  if (!p || p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads || p->q_len < 1 ||
+      p->batch < 0 || p->max_seqlen < 0)
+    return 0;
   return workspace_bytes(p, choose_partition(p));
 }
 
@@ -404,7 +825,7 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
   if (rc != HEXKV_OK || p->batch == 0) return rc;
   const int part = choose_partition(p);
   const int G = kernel_group(p->q_heads / p->kv_heads);
-  const int max_parts = std::max(1, (p->max_seqlen + part - 1) / part);
+  const int64_t max_parts = max_parts_of(p, part);
   const size_t need = workspace_bytes(p, part);
   if (need > 0 && (!workspace || ws_bytes < need))
     return fail(HEXKV_EWORKSPACE, "hexkv_attend: workspace of %zu bytes needed, %zu given", need,
@@ -433,32 +854,31 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
   a.kv_heads = p->kv_heads;
   a.group = p->q_heads / p->kv_heads;
   a.part = part;
-  a.max_parts = max_parts;
+  a.max_parts = static_cast<int32_t>(max_parts);
   a.max_seqlen = p->max_seqlen;
   a.capacity = p->capacity;
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
-  a.ws_o = static_cast<float *>(workspace);
-  const int64_t slots = rows * p->q_heads * max_parts;
-  a.ws_ml = need > 0 ? a.ws_o + slots * p->head_dim : nullptr;
+  a.ws_o = nullptr;
+  a.ws_ml = nullptr;
+  if (need > 0) {
+    a.ws_o = static_cast<float *>(workspace);
+    a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
+  }
 
-  dim3 grid(static_cast<unsigned>(max_parts), static_cast<unsigned>(p->q_heads / G),
-            static_cast<unsigned>(rows));
-  const size_t smem = sizeof(float) * std::max<size_t>(static_cast<size_t>(part) * G,
-                                                       static_cast<size_t>(kAttWaves) * G * p->head_dim);
+  // Workgroups reach the 8 XCDs round-robin by linear index, and the later
+  // partitions exist only in long rows.  With an even partition count the
+  // same partition indices would always land on the same XCDs (measured 1.6x
+  // slower at 32 than at 31); an odd count rotates them across the XCDs from
+  // one (head group, row) to the next.  The extra column is empty.
+  const unsigned grid_x = static_cast<unsigned>(max_parts | 1);
+  dim3 grid(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool mfma = use_mfma(p, G);
   switch (p->dtype) {
-    case HEXKV_BF16: rc = dispatch_d<__bf16>(p->head_dim, G, a, grid, smem, s); break;
-    case HEXKV_F16: rc = dispatch_d<_Float16>(p->head_dim, G, a, grid, smem, s); break;
-    default: rc = dispatch_d<float>(p->head_dim, G, a, grid, smem, s); break;
+    case HEXKV_BF16: rc = dispatch_d<__bf16>(p->head_dim, G, a, grid, mfma, s); break;
+    case HEXKV_F16: rc = dispatch_d<_Float16>(p->head_dim, G, a, grid, mfma, s); break;
+    default: rc = dispatch_d<float>(p->head_dim, G, a, grid, mfma, s); break;
   }
   if (rc != HEXKV_OK) return rc;
-  rc = check_launch("hexkv_attend");
-  if (rc != HEXKV_OK || max_parts <= 1) return rc;
-  dim3 cgrid(static_cast<unsigned>(p->q_heads), static_cast<unsigned>(rows));
-  switch (p->dtype) {
-    case HEXKV_BF16: combine_kernel<__bf16><<<cgrid, 64, 0, s>>>(a, p->head_dim); break;
-    case HEXKV_F16: combine_kernel<_Float16><<<cgrid, 64, 0, s>>>(a, p->head_dim); break;
-    default: combine_kernel<float><<<cgrid, 64, 0, s>>>(a, p->head_dim); break;
-  }
-  return check_launch("hexkv_attend(combine)");
+  return check_launch("hexkv_attend");
 }

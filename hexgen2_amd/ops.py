@@ -160,7 +160,7 @@ def append_kv(cache: torch.Tensor, kv_new: torch.Tensor, positions: Optional[tor
 
 
 def _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, causal,
-                   softmax_scale, partition) -> _lib.AttendParams:
+                   softmax_scale, partition, kernel="auto") -> _lib.AttendParams:
     if q.dim() != 4 or cache.dim() != 5 or cache.shape[2] != 2:
         raise ValueError("q must be [batch, q_len, q_heads, head_dim] and the cache "
                          "[batch, capacity, 2, kv_heads, head_dim]")
@@ -201,13 +201,16 @@ def _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, caus
             raise ValueError("kv_new must be contiguous [batch, 2, kv_heads, head_dim]")
         p.kv_new = kv_new.data_ptr()
     p.partition = int(partition)
+    if kernel not in _lib.KERNELS:
+        raise ValueError(f"kernel must be one of {sorted(_lib.KERNELS)}, got {kernel!r}")
+    p.kernel = _lib.KERNELS[kernel]
     return p
 
 
 def attend_workspace_bytes(q: torch.Tensor, cache: torch.Tensor, max_seqlen: int,
-                           partition: int = 0) -> int:
+                           partition: int = 0, kernel: str = "auto") -> int:
     out = q  # geometry only
-    p = _attend_params(q, cache, out, None, max_seqlen, max_seqlen, None, False, None, partition)
+    p = _attend_params(q, cache, out, None, max_seqlen, max_seqlen, None, False, None, partition, kernel)
     return int(_lib.load().hexkv_attend_workspace_bytes(ctypes.byref(p)))
 
 
@@ -215,7 +218,8 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
                      seqlens: Optional[torch.Tensor] = None, seqlen_bias: int = 0,
                      kv_new: Optional[torch.Tensor] = None, causal: bool = False,
                      softmax_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                     workspace: Optional[torch.Tensor] = None, partition: int = 0) -> torch.Tensor:
+                     workspace: Optional[torch.Tensor] = None, partition: int = 0,
+                     kernel: str = "auto") -> torch.Tensor:
     """Attention of ``q [B, q_len, Hq, D]`` over a cache ``[B, S, 2, Hkv, D]``.
 
     Sequence b attends to ``len_b = seqlens[b] + seqlen_bias`` keys (the
@@ -224,13 +228,15 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     ``len_b + 1`` keys are attended.  ``max_seqlen`` is a host bound on the
     attended length (including that +1).  GQA maps q head h to KV head
     ``h // (Hq // Hkv)`` (mha.py:223-224); ``softmax_scale`` defaults to
-    ``D ** -0.5`` (gpt.py:72).
+    ``D ** -0.5`` (gpt.py:72).  ``kernel`` picks the score kernel: "valu"
+    (packed dot products), "mfma" (the GQA group on the matrix cores, 16-bit
+    only) or "auto" (the library's choice).
     """
     _require_device(q, cache)
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     p = _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, causal,
-                       softmax_scale, partition)
+                       softmax_scale, partition, kernel)
     lib = _lib.load()
     need = int(lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
     ws_ptr, ws_bytes = None, 0
@@ -256,10 +262,10 @@ class AttendPlan:
     def __init__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *,
                  max_seqlens: Sequence[int], seqlens: Optional[torch.Tensor] = None,
                  kv_new: Optional[torch.Tensor] = None, softmax_scale: Optional[float] = None,
-                 partition: int = 0):
+                 partition: int = 0, kernel: str = "auto"):
         _require_device(q, cache, out)
         self.params = _attend_params(q, cache, out, seqlens, 0, max(max_seqlens), kv_new, False,
-                                     softmax_scale, partition)
+                                     softmax_scale, partition, kernel)
         self.lib = _lib.load()
         need = 0
         for m in max_seqlens:

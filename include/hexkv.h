@@ -45,6 +45,14 @@ enum hexkv_dtype {
   HEXKV_F32 = 2   /* torch.float32  */
 };
 
+/* Attention kernels.  AUTO picks MFMA for 16-bit data with head_dim >= 64
+ * and 8+ query heads per KV head, VALU otherwise. */
+enum hexkv_kernel {
+  HEXKV_KERNEL_AUTO = 0,
+  HEXKV_KERNEL_VALU = 1, /* packed dot products on the vector ALUs     */
+  HEXKV_KERNEL_MFMA = 2  /* GQA group dot products on the matrix cores */
+};
+
 enum hexkv_status {
   HEXKV_OK = 0,
   HEXKV_EINVAL = -1,       /* bad argument: shape, length, alignment, null */
@@ -161,10 +169,13 @@ typedef struct hexkv_attend_params {
   const void *kv_new;
   /* Split-K partition size in positions; 0 = chosen by the library. */
   int partition;
+  /* enum hexkv_kernel: which kernel computes the scores. */
+  int kernel;
 } hexkv_attend_params;
 
 /* Workspace bytes hexkv_attend needs for these parameters (0 when one
- * partition covers every sequence). */
+ * partition covers every sequence).  The workspace is scratch (partial
+ * outputs of the split-K merge); calls sharing one must not overlap. */
 size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p);
 
 /*

@@ -2,7 +2,9 @@
 
 Tolerances (max-abs, inputs rounded to the dtype first, oracle in float64):
 fp16 2e-3, bf16 8e-3, fp32 2e-5.  The fused append must also write the new
-row bit-exactly and touch nothing else.
+row bit-exactly and touch nothing else.  Both score kernels are checked: the
+VALU kernel (every dtype and head_dim) and the MFMA kernel (16-bit,
+head_dim >= 64).
 """
 import numpy as np
 import pytest
@@ -54,15 +56,23 @@ GEOMETRIES = [
 ]
 
 
-@pytest.mark.parametrize("hq,hkv,d,dtype", GEOMETRIES)
-def test_ragged_lengths_within_tolerance(device, hq, hkv, d, dtype):
-    lens = [1, 63, 64, 65, 700, 1500, 2049]
+def kernels_for(dtype, d):
+    return ["valu", "mfma"] if dtype != torch.float32 and d >= 64 else ["valu"]
+
+
+CASES = [(hq, hkv, d, dtype, kernel) for hq, hkv, d, dtype in GEOMETRIES for kernel in kernels_for(dtype, d)]
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel", CASES)
+def test_ragged_lengths_within_tolerance(device, hq, hkv, d, dtype, kernel):
+    lens = [1, 15, 16, 17, 63, 64, 65, 700, 1500, 2049]
     cap = 2112
-    print(f"attend hq={hq} hkv={hkv} d={d} {dtype} lens={lens}", flush=True)
+    print(f"attend {kernel} hq={hq} hkv={hkv} d={d} {dtype} lens={lens}", flush=True)
     q, cache = make(len(lens), cap, hq, hkv, d, dtype, 1, device)
     seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
-    for partition in (0, 64, 512):
-        out = ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=partition)
+    for partition in (0, 64, 192, 512):
+        out = ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=partition,
+                                   kernel=kernel)
         torch.cuda.synchronize()
         check(out, q, cache, lens, dtype)
 
@@ -70,8 +80,20 @@ def test_ragged_lengths_within_tolerance(device, hq, hkv, d, dtype):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_uniform_length_and_scale(device, dtype):
     q, cache = make(3, 300, 16, 4, 128, dtype, 2, device)
-    out = ops.decode_attention(q, cache, max_seqlen=257, seqlen_bias=257, softmax_scale=0.05)
-    check(out, q, cache, [257] * 3, dtype, scale=0.05)
+    for kernel in kernels_for(dtype, 128):
+        out = ops.decode_attention(q, cache, max_seqlen=257, seqlen_bias=257, softmax_scale=0.05, kernel=kernel)
+        check(out, q, cache, [257] * 3, dtype, scale=0.05)
+
+
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_large_scores_rescale_running_max(device, kernel):
+    # scores growing along the sequence force repeated rescales of the
+    # running maximum; a large scale makes them span hundreds of log2 units
+    q, cache = make(2, 600, 8, 2, 128, torch.bfloat16, 13, device)
+    ramp = torch.linspace(0.1, 4.0, 600, device=device)[None, :, None, None]
+    cache[:, :, 0] = (cache[:, :, 0].float() * ramp).to(torch.bfloat16)
+    out = ops.decode_attention(q, cache, max_seqlen=600, seqlen_bias=600, softmax_scale=0.5, kernel=kernel)
+    check(out, q, cache, [600, 600], torch.bfloat16, scale=0.5)
 
 
 def test_single_key_returns_value_exactly(device):
@@ -99,59 +121,79 @@ def test_zero_length_rows_give_zeros(device):
     check(out[1:2], q[1:2], cache[1:2], [5], torch.float16)
 
 
-@pytest.mark.parametrize("hq,hkv,d,dtype", [(32, 8, 128, torch.bfloat16), (32, 4, 64, torch.float16),
-                                           (4, 4, 16, torch.float32), (32, 2, 128, torch.bfloat16)])
-def test_fused_append_writes_row_and_attends_it(device, hq, hkv, d, dtype):
-    lens = [0, 5, 63, 64, 1023, 1024, 3000]
+FUSED = [(32, 8, 128, torch.bfloat16, "valu"), (32, 8, 128, torch.bfloat16, "mfma"),
+         (32, 4, 64, torch.float16, "valu"), (32, 4, 64, torch.float16, "mfma"),
+         (4, 4, 16, torch.float32, "valu"), (32, 2, 128, torch.bfloat16, "mfma"),
+         (8, 1, 256, torch.bfloat16, "mfma"), (8, 1, 256, torch.bfloat16, "valu")]
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel", FUSED)
+def test_fused_append_writes_row_and_attends_it(device, hq, hkv, d, dtype, kernel):
+    lens = [0, 5, 15, 16, 63, 64, 1023, 1024, 3000]
     cap = 3100
+    print(f"fused {kernel} hq={hq} hkv={hkv} d={d} {dtype}", flush=True)
     q, cache = make(len(lens), cap, hq, hkv, d, dtype, 6, device)
     g = torch.Generator(device=device).manual_seed(7)
     kv_new = torch.randn((len(lens), 2, hkv, d), generator=g, device=device).to(dtype)
     before = bits(cache)
     seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
-    out = ops.decode_attention(q, cache, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new)
+    out = ops.decode_attention(q, cache, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new, kernel=kernel)
     torch.cuda.synchronize()
     want_cache = oracle.append(before, bits(kv_new), lens)
     np.testing.assert_array_equal(bits(cache), want_cache)
     check(out, q, cache, [n + 1 for n in lens], dtype)
 
 
-def test_fused_append_with_bias_matches_unfused(device):
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_fused_append_with_bias_matches_unfused(device, kernel):
     q, cache = make(4, 200, 32, 8, 128, torch.bfloat16, 8, device)
     kv_new = torch.randn((4, 2, 8, 128), device=device).to(torch.bfloat16)
     base = torch.tensor([10, 0, 150, 98], dtype=torch.int32, device=device)
     c1, c2 = cache.clone(), cache.clone()
-    o1 = ops.decode_attention(q, c1, max_seqlen=156, seqlens=base, seqlen_bias=5, kv_new=kv_new)
+    o1 = ops.decode_attention(q, c1, max_seqlen=156, seqlens=base, seqlen_bias=5, kv_new=kv_new, kernel=kernel)
     ops.append_kv(c2, kv_new.reshape(4, -1), base, position_bias=5)
-    o2 = ops.decode_attention(q, c2, max_seqlen=156, seqlens=base, seqlen_bias=6)
+    o2 = ops.decode_attention(q, c2, max_seqlen=156, seqlens=base, seqlen_bias=6, kernel=kernel)
     assert torch.equal(c1, c2)
-    assert torch.equal(o1, o2)
+    # the same keys in the same order; only the summation grouping may differ
+    torch.testing.assert_close(o1, o2, rtol=0, atol=8e-3)
+    check(o1, q, c2, [n + 6 for n in [10, 0, 150, 98]], torch.bfloat16)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-def test_causal_prefill_rows(device, dtype):
-    q, cache = make(2, 40, 4, 2, 32, dtype, 9, device, q_len=7)
-    out = ops.decode_attention(q, cache, max_seqlen=40, seqlen_bias=7, causal=True)
+@pytest.mark.parametrize("dtype,d,kernel", [(torch.float32, 32, "valu"), (torch.float16, 32, "valu"),
+                                            (torch.float16, 64, "mfma"), (torch.bfloat16, 128, "mfma")])
+def test_causal_prefill_rows(device, dtype, d, kernel):
+    q, cache = make(2, 40, 4, 2, d, dtype, 9, device, q_len=7)
+    out = ops.decode_attention(q, cache, max_seqlen=40, seqlen_bias=7, causal=True, kernel=kernel)
     check(out, q, cache, [7, 7], dtype, causal=True)
     seqlens = torch.tensor([30, 7], dtype=torch.int32, device=device)
-    out = ops.decode_attention(q, cache, max_seqlen=40, seqlens=seqlens, causal=True)
+    out = ops.decode_attention(q, cache, max_seqlen=40, seqlens=seqlens, causal=True, kernel=kernel)
     check(out, q, cache, [30, 7], dtype, causal=True)
 
 
-def test_strided_cache_view_batch_offset(device):
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_strided_cache_view_batch_offset(device, kernel):
     # the view _update_kv_cache returns: cache[b0:b1, :offset+1]
     q, cache = make(5, 64, 8, 2, 64, torch.float16, 10, device)
     view = cache[1:4, :33]
-    out = ops.decode_attention(q[1:4], view, max_seqlen=33, seqlen_bias=33)
+    out = ops.decode_attention(q[1:4], view, max_seqlen=33, seqlen_bias=33, kernel=kernel)
     check(out, q[1:4], view, [33] * 3, torch.float16)
 
 
-def test_repeatable(device):
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_repeatable(device, kernel):
     q, cache = make(8, 4096, 32, 8, 128, torch.bfloat16, 11, device)
     lens = torch.randint(1, 4096, (8,), dtype=torch.int32, device=device)
-    a = ops.decode_attention(q, cache, max_seqlen=4096, seqlens=lens)
-    b = ops.decode_attention(q, cache, max_seqlen=4096, seqlens=lens)
+    a = ops.decode_attention(q, cache, max_seqlen=4096, seqlens=lens, kernel=kernel)
+    b = ops.decode_attention(q, cache, max_seqlen=4096, seqlens=lens, kernel=kernel)
     assert torch.equal(a, b)
+
+
+def test_valu_and_mfma_agree(device):
+    q, cache = make(6, 3000, 32, 8, 128, torch.bfloat16, 14, device)
+    lens = torch.tensor([1, 17, 300, 1025, 2999, 2048], dtype=torch.int32, device=device)
+    a = ops.decode_attention(q, cache, max_seqlen=3000, seqlens=lens, kernel="valu")
+    b = ops.decode_attention(q, cache, max_seqlen=3000, seqlens=lens, kernel="mfma")
+    torch.testing.assert_close(a.float(), b.float(), rtol=0, atol=8e-3)
 
 
 def test_validation_errors(device):
@@ -163,3 +205,11 @@ def test_validation_errors(device):
         ops.decode_attention(qq, cc, max_seqlen=4, seqlen_bias=4)  # head_dim 48 not compiled
     with pytest.raises(ValueError):
         ops.decode_attention(q.float(), cache, max_seqlen=4, seqlen_bias=4)  # dtype mismatch
+    with pytest.raises(NotImplementedError):
+        qq, cc = make(1, 8, 2, 1, 32, torch.float16, 0, device)
+        ops.decode_attention(qq, cc, max_seqlen=4, seqlen_bias=4, kernel="mfma")  # head_dim < 64
+    with pytest.raises(NotImplementedError):
+        qq, cc = make(1, 8, 2, 1, 64, torch.float32, 0, device)
+        ops.decode_attention(qq, cc, max_seqlen=4, seqlen_bias=4, kernel="mfma")  # fp32
+    with pytest.raises(ValueError):
+        ops.decode_attention(q, cache, max_seqlen=4, seqlen_bias=4, softmax_scale=-1.0)

@@ -19,6 +19,10 @@
 
 namespace hexkv {
 
+// 256 threads x 4 vectors of 16 bytes in flight per workgroup.  A chunked
+// copy of this shape moves 5.55 TB/s (read + write) on MI355X, a
+// device-to-device hipMemcpy 4.90; 512 threads measured 2% faster on one
+// contiguous 8 GiB copy but 2.5% slower on the ragged pack/unpack.
 constexpr int kCopyThreads = 256;
 constexpr int kCopyUnroll = 4;
 

@@ -368,20 +368,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   // Merge the GPW lane groups of this wave (lanes with equal `sub`).
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float mw = m[g];
-#pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) mw = fmaxf(mw, __shfl_xor(mw, off));
+    const float mw = max_from<LPP>(m[g]);
     const float c = fast_exp2(m[g] - mw);
     m[g] = mw;
-    l[g] *= c;
+    l[g] = sum_from<LPP>(l[g] * c);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[g][e] *= c;
-#pragma unroll
-    for (int off = LPP; off < 64; off <<= 1) {
-      l[g] += __shfl_xor(l[g], off);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
-    }
+    for (int e = 0; e < EPL; ++e) acc[g][e] = sum_from<LPP>(acc[g][e] * c);
   }
   if (lane < LPP) {
 #pragma unroll
@@ -517,10 +509,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
       if constexpr (MODE == 1) s[e] = i0 + 4 * kg + e < w.n_cache ? s[e] : -INFINITY;
       if constexpr (MODE == 2) s[e] = (kg == 0 && e == 0) ? s[e] : -INFINITY;
     }
-    float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    mt *= scale;
+    float mt = max_from<16>(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))) * scale;
     const bool up = head_lane && mt > m + kRescaleSlack;
     if (__any(up)) {
       const float mnew = up ? mt : m;
@@ -570,14 +559,11 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
 
   // Wave totals: l over the 4 kg lanes of each head, o over the value lanes
   // of each slice.
-  lp += __shfl_xor(lp, 16);
-  lp += __shfl_xor(lp, 32);
+  lp = sum_from<16>(lp);
 #pragma unroll
-  for (int off = VLPP; off < 64; off <<= 1)
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+    for (int e = 0; e < 8; ++e) acc[g][e] = sum_from<VLPP>(acc[g][e]);
   if (lane < VLPP) {
 #pragma unroll
     for (int g = 0; g < G; ++g)

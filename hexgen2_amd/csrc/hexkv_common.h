@@ -54,6 +54,31 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Butterfly step over lanes l and l ^ OFF (ds_bpermute).
+template <int OFF>
+__device__ __forceinline__ float xor_sum(float v) {
+  return v + __shfl_xor(v, OFF);
+}
+
+template <int OFF>
+__device__ __forceinline__ float xor_max(float v) {
+  return fmaxf(v, __shfl_xor(v, OFF));
+}
+
+// xor_sum / xor_max over every offset in [FROM, 64): the total over the
+// lanes that agree in their low log2(FROM) bits.
+template <int FROM>
+__device__ __forceinline__ float sum_from(float v) {
+  if constexpr (FROM < 64) return sum_from<FROM * 2>(xor_sum<FROM>(v));
+  else return v;
+}
+
+template <int FROM>
+__device__ __forceinline__ float max_from(float v) {
+  if constexpr (FROM < 64) return max_from<FROM * 2>(xor_max<FROM>(v));
+  else return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));

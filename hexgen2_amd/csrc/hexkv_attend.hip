@@ -216,7 +216,7 @@ __device__ __forceinline__ void lazy_rescale(const float (&mt)[G], float (&m)[G]
 
 // ------------------------------------------------------------- VALU path ---
 
-template <typename T, int D, int G, int U>
+template <typename T, int D, int G, int U, bool PF = true>
 __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendArgs a) {
   using E = Elem<T>;
   using L = Lanes<T, D>;
@@ -256,12 +256,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
   }
 
-  // One iteration: U slots of one position per lane group.  TAIL clamps the
-  // positions past n_cache to the last cached one (finite data) and masks
-  // their scores.
-  auto step = [&](int i0, auto tail) {
+  // One iteration covers U slots of one position per lane group.  `fetch`
+  // issues its loads; TAIL clamps the positions past n_cache to the last
+  // cached one (finite data) and `consume` masks their scores.
+  using Slots = u32x4[U][NV];
+  auto fetch = [&](int i0, Slots &kr, Slots &vr, auto tail) {
     constexpr bool TAIL = decltype(tail)::value;
-    u32x4 kr[U][NV], vr[U][NV];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       uint32_t off;
@@ -277,6 +277,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
         vr[u][v] = load16(vseq, off + v * 16);
       }
     }
+  };
+  auto consume = [&](int i0, const Slots &kr, const Slots &vr, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
     float sc[U][G];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -319,9 +322,41 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
     }
   };
 
+  // Full iterations, software-pipelined PF deep: the loads of iteration
+  // i + 1 are in flight while iteration i computes.  Then the tail.
+  const int n_full = w.n_cache / STEP * STEP;
   int i0 = 0;
-  for (; i0 + STEP <= w.n_cache; i0 += STEP) step(i0, std::false_type{});
-  if (i0 < w.n_cache) step(i0, std::true_type{});
+  if constexpr (PF) {
+    if (n_full > 0) {
+      Slots ka, va;
+      fetch(0, ka, va, std::false_type{});
+      for (; i0 + STEP < n_full; i0 += STEP) {
+        Slots kb, vb;
+        fetch(i0 + STEP, kb, vb, std::false_type{});
+        consume(i0, ka, va, std::false_type{});
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+            ka[u][v] = kb[u][v];
+            va[u][v] = vb[u][v];
+          }
+      }
+      consume(i0, ka, va, std::false_type{});
+      i0 += STEP;
+    }
+  } else {
+    for (; i0 < n_full; i0 += STEP) {
+      Slots kr, vr;
+      fetch(i0, kr, vr, std::false_type{});
+      consume(i0, kr, vr, std::false_type{});
+    }
+  }
+  if (i0 < w.n_cache) {
+    Slots kr, vr;
+    fetch(i0, kr, vr, std::true_type{});
+    consume(i0, kr, vr, std::true_type{});
+  }
 
   if (w.has_new) {
     // The new row: attended by lane group 0 from kv_new, written to the cache
@@ -739,12 +774,14 @@ static int validate(const hexkv_attend_params *p) {
   return HEXKV_OK;
 }
 
-// Load slots per lane group and iteration of the VALU kernel.  One slot
-// keeps the registers low enough for more resident waves, which measured
-// faster than 2 or 4 slots per wave at the partition sizes chosen above.
+// Load slots per lane group and iteration of the VALU kernel (with the next
+// iteration's loads in flight): 2 for one 16-byte vector per lane, 1 for two
+// or more.  Measured at Llama-3-8B, 1024-position partitions: 2 slots +
+// prefetch 171.4 us, 4 slots + prefetch 172.7, 2 slots without 178.3,
+// 1 slot without 187.8.
 template <typename T, int D, int G>
 constexpr int slots() {
-  return 1;
+  return Lanes<T, D>::NV >= 2 ? 1 : 2;
 }
 
 // Kernel choice: the MFMA kernel for 16-bit data with head_dim >= 64 and 8+

@@ -499,10 +499,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
 
-  // One tile of 16 positions starting at p0 + i0 (kv_new for the new row).
-  auto tile = [&](int i0, auto mode) {
-    constexpr int MODE = decltype(mode)::value;  // 0 full, 1 tail, 2 new row
-    u32x4 kr[NJ], vr[UV];
+  // One tile of 16 positions starting at p0 + i0: `fetch` issues its loads
+  // (MODE 0 full, 1 tail: positions past n_cache clamped to the last cached
+  // one, 2: the new row from kv_new, written to the cache by the writer);
+  // `consume` computes it (masking what MODE 1 and 2 do not attend).
+  auto fetch = [&](int i0, u32x4 (&kr)[NJ], u32x4 (&vr)[UV], auto mode) {
+    constexpr int MODE = decltype(mode)::value;
     if constexpr (MODE == 2) {
       const char *knew = static_cast<const char *>(a.kv_new) +
                          ((static_cast<int64_t>(w.b) * 2 * a.kv_heads + w.hk) * D) * static_cast<int64_t>(sizeof(T));
@@ -534,6 +536,9 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
 #pragma unroll
       for (int u = 0; u < UV; ++u) vr[u] = load16(vseq, voff[u]);
     }
+  };
+  auto consume = [&](int i0, const u32x4 (&kr)[NJ], const u32x4 (&vr)[UV], auto mode) {
+    constexpr int MODE = decltype(mode)::value;
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NJ; ++j) c = Mfma<T>::mma(kr[j], qb[j], c);
@@ -585,12 +590,36 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
     __builtin_amdgcn_wave_barrier();
   };
 
-  // Tiles of 16 positions, dealt round-robin to the waves.
+  // Tiles of 16 positions, dealt round-robin to the waves; the next full
+  // tile's loads are in flight while the current one computes.
+  using Full = std::integral_constant<int, 0>;
   const int full_tiles = w.n_cache / 16;
   int ti = wave;
-  for (; ti < full_tiles; ti += kAttWaves) tile(ti * 16, std::integral_constant<int, 0>{});
-  if (ti * 16 < w.n_cache) tile(ti * 16, std::integral_constant<int, 1>{});
-  if (w.has_new && wave == 0) tile(0, std::integral_constant<int, 2>{});
+  if (ti < full_tiles) {
+    u32x4 ka[NJ], va[UV];
+    fetch(ti * 16, ka, va, Full{});
+    for (; ti + kAttWaves < full_tiles; ti += kAttWaves) {
+      u32x4 kb[NJ], vb[UV];
+      fetch((ti + kAttWaves) * 16, kb, vb, Full{});
+      consume(ti * 16, ka, va, Full{});
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) ka[j] = kb[j];
+#pragma unroll
+      for (int u = 0; u < UV; ++u) va[u] = vb[u];
+    }
+    consume(ti * 16, ka, va, Full{});
+    ti += kAttWaves;
+  }
+  if (ti * 16 < w.n_cache) {
+    u32x4 kr[NJ], vr[UV];
+    fetch(ti * 16, kr, vr, std::integral_constant<int, 1>{});
+    consume(ti * 16, kr, vr, std::integral_constant<int, 1>{});
+  }
+  if (w.has_new && wave == 0) {
+    u32x4 kr[NJ], vr[UV];
+    fetch(0, kr, vr, std::integral_constant<int, 2>{});
+    consume(0, kr, vr, std::integral_constant<int, 2>{});
+  }
 
   // Wave totals: l over the 4 kg lanes of each head, o over the value lanes
   // of each slice.
@@ -613,21 +642,24 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
   finish_work<T, D, G>(a, w, s_acc, s_m, s_l);
 }
 
-// Merges the partitions of one (query row, head group) of a split row:
+// Merges the partitions of one (query row, query head) of a split row:
 // o = sum_p w_p o_p with w_p = 2^(m_p - max m) / sum_p 2^(m_p - max m) l_p.
-// TPH lanes per head reduce (max, sum) over the partitions and stage the
-// weights in LDS; then each thread merges its outputs with all partition
-// loads of a chunk issued before they are used.
+// One wave reduces (max, sum) over the partitions and stages the weights in
+// LDS; the 256 threads then split the partitions into 256 / D slices of D
+// outputs each (all loads of a slice issued 8 at a time) and add the slices
+// through LDS.  One workgroup per (head, row) keeps the per-workgroup chain
+// short when a few long rows carry many partitions.
 constexpr int kCombineChunk = 256;  // partitions whose weights sit in LDS at once
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a) {
   using E = Elem<T>;
-  constexpr int TPH = 256 / G < 64 ? 256 / G : 64;  // threads per head in the reduction
-  constexpr int PER = (G * D + kAttThreads - 1) / kAttThreads;  // outputs per thread
-  __shared__ float s_w[G][kCombineChunk];
-  __shared__ float s_mx[G], s_inv[G];
-  const int row = blockIdx.y, qh0 = blockIdx.x * G;
+  constexpr int SL = kAttThreads / D >= 1 ? kAttThreads / D : 1;  // partition slices
+  constexpr int PER = (D + kAttThreads - 1) / kAttThreads;        // outputs per thread (D > 256)
+  __shared__ float s_w[kCombineChunk];
+  __shared__ float s_red[SL][D];
+  __shared__ float s_mx, s_inv;
+  const int h = blockIdx.x, row = blockIdx.y;
   const int b = row / a.q_len, t = row - b * a.q_len;
   int pos_new;
   const int len = row_length(a, b, t, &pos_new);
@@ -635,57 +667,61 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
   const int nparts = (len + a.part - 1) / a.part;
   if (nparts <= 1) return;
   const int tid = threadIdx.x;
-  const int64_t slot0 = (static_cast<int64_t>(row) * a.q_heads + qh0) * a.max_parts;
-  const int hg = tid / TPH, hj = tid % TPH;
-  if (hg < G) {
-    const float *ml = a.ws_ml + (slot0 + static_cast<int64_t>(hg) * a.max_parts) * 2;
+  const int64_t base = (static_cast<int64_t>(row) * a.q_heads + h) * a.max_parts;
+  const float *ml = a.ws_ml + base * 2;
+  if (tid < 64) {
     float mx = kNoScore;
-    for (int p = hj; p < nparts; p += TPH) mx = fmaxf(mx, ml[2 * p]);
-#pragma unroll
-    for (int off = TPH / 2; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    for (int p = tid; p < nparts; p += 64) mx = fmaxf(mx, ml[2 * p]);
+    mx = max_from<1>(mx);
     float sum = 0.f;
-    for (int p = hj; p < nparts; p += TPH) sum = fmaf(fast_exp2(ml[2 * p] - mx), ml[2 * p + 1], sum);
-#pragma unroll
-    for (int off = TPH / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-    if (hj == 0) {
-      s_mx[hg] = mx;
-      s_inv[hg] = 1.f / sum;
+    for (int p = tid; p < nparts; p += 64) sum = fmaf(fast_exp2(ml[2 * p] - mx), ml[2 * p + 1], sum);
+    sum = sum_from<1>(sum);
+    if (tid == 0) {
+      s_mx = mx;
+      s_inv = 1.f / sum;
     }
   }
+  const int d0 = tid % D, sl = tid / D;
   float acc[PER];
 #pragma unroll
   for (int k = 0; k < PER; ++k) acc[k] = 0.f;
   for (int c0 = 0; c0 < nparts; c0 += kCombineChunk) {
     const int nc = min(kCombineChunk, nparts - c0);
-    __syncthreads();  // s_mx/s_inv ready; previous chunk's weights consumed
-    if (hg < G) {
-      const float *ml = a.ws_ml + (slot0 + static_cast<int64_t>(hg) * a.max_parts + c0) * 2;
-      for (int p = hj; p < nc; p += TPH) s_w[hg][p] = fast_exp2(ml[2 * p] - s_mx[hg]) * s_inv[hg];
-    }
+    __syncthreads();  // s_mx/s_inv ready; the previous chunk's weights consumed
+    for (int p = tid; p < nc; p += kAttThreads) s_w[p] = fast_exp2(ml[2 * (c0 + p)] - s_mx) * s_inv;
     __syncthreads();
+    if (sl < SL) {
 #pragma unroll
-    for (int k = 0; k < PER; ++k) {
-      const int i = tid + k * kAttThreads;
-      if (i < G * D) {
-        const int g = i / D, d = i - g * D;
-        const float *o = a.ws_o + (slot0 + static_cast<int64_t>(g) * a.max_parts + c0) * D + d;
-        int p = 0;
-        for (; p + 8 <= nc; p += 8) {
+      for (int k = 0; k < PER; ++k) {
+        const float *o = a.ws_o + (base + c0) * D + d0 + k * kAttThreads;
+        int p = sl;
+        for (; p + 7 * SL < nc; p += 8 * SL) {
           float v[8];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) v[u] = o[static_cast<int64_t>(p + u) * D];
+          for (int u = 0; u < 8; ++u) v[u] = o[static_cast<int64_t>(p + u * SL) * D];
 #pragma unroll
-          for (int u = 0; u < 8; ++u) acc[k] = fmaf(s_w[g][p + u], v[u], acc[k]);
+          for (int u = 0; u < 8; ++u) acc[k] = fmaf(s_w[p + u * SL], v[u], acc[k]);
         }
-        for (; p < nc; ++p) acc[k] = fmaf(s_w[g][p], o[static_cast<int64_t>(p) * D], acc[k]);
+        for (; p < nc; p += SL) acc[k] = fmaf(s_w[p], o[static_cast<int64_t>(p) * D], acc[k]);
       }
     }
   }
-  T *out_row = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + qh0 * D;
+  T *out = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + static_cast<int64_t>(h) * D;
+  if constexpr (SL > 1) {
+    if (sl < SL) s_red[sl][d0] = acc[0];
+    __syncthreads();
+    if (tid < D) {
+      float o = 0.f;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const int i = tid + k * kAttThreads;
-    if (i < G * D) out_row[i] = E::from_float(acc[k]);
+      for (int k = 0; k < SL; ++k) o += s_red[k][tid];
+      out[tid] = E::from_float(o);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int d = d0 + k * kAttThreads;
+      if (sl == 0 && d < D) out[d] = E::from_float(acc[k]);
+    }
   }
 }
 
@@ -701,18 +737,19 @@ static int kernel_group(int group) {
 }
 
 // Partition size: about (rows x head groups x positions) / 2048 positions,
-// as a power of two in [64, 1024], counting half of max_seqlen per row
-// (ragged batches average about that).  Measured on MI355X: Llama-3-8B's
-// shape (64 rows x 8 groups, lengths to 8K) is fastest at 1024, Llama-2-7B's
-// (8 x 32, to 2K) at 128-512, the Llama-2-70B TP-8 share (32 x 1, to 4K) at
-// 128-256 and TinyLlama (1 x 4, 512) at 64.
+// as a power of two in [128, 1024], counting half of max_seqlen per row
+// (ragged batches average about that).  Measured on MI355X (attention +
+// combine per layer): Llama-3-8B's shape (64 rows x 8 groups, lengths to 8K)
+// is fastest at 768-1024, Llama-2-7B's (8 x 32, to 2K) at 128-512, the
+// Llama-2-70B TP-8 share (32 x 1, to 4K) at 128-256 and TinyLlama (1 x 4,
+// 512) at 128.
 static int choose_partition(const hexkv_attend_params *p) {
   if (p->partition > 0) return p->partition;
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
   const int64_t groups = p->q_heads / kernel_group(p->q_heads / p->kv_heads);
   const int64_t half = std::max<int64_t>(1, (p->max_seqlen + 1) / 2);
   const int64_t want = rows * groups * half / 2048;
-  int part = 64;
+  int part = 128;
   while (part < 1024 && part < want) part <<= 1;
   return part;
 }
@@ -803,7 +840,7 @@ static void launch(const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
   } else {
     attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
   }
-  if (a.max_parts > 1) combine_kernel<T, D, G><<<dim3(grid.y, grid.z), kAttThreads, 0, s>>>(a);
+  if (a.max_parts > 1) combine_kernel<T, D, G><<<dim3(a.q_heads, grid.z), kAttThreads, 0, s>>>(a);
 }
 
 template <typename T, int D>

@@ -19,7 +19,8 @@ MAX_SEQS_PER_LAUNCH = 256
 
 # Every symbol the header declares; tests check the library exports them all.
 EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "hexkv_append",
-           "hexkv_attend_workspace_bytes", "hexkv_attend")
+           "hexkv_attend_workspace_bytes", "hexkv_attend", "hexkv_ipc_export", "hexkv_ipc_open",
+           "hexkv_ipc_close", "hexkv_ipc_dlpack")
 
 
 class AttendParams(ctypes.Structure):
@@ -36,6 +37,11 @@ class AttendParams(ctypes.Structure):
         ("seqlens_dev", ctypes.c_void_p), ("seqlen_bias", ctypes.c_int32), ("max_seqlen", ctypes.c_int32),
         ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int), ("kernel", ctypes.c_int),
     ]
+
+
+class IpcHandle(ctypes.Structure):
+    """Mirror of ``hexkv_ipc_handle``."""
+    _fields_ = [("bytes", ctypes.c_ubyte * 64)]
 
 
 class HexKVError(RuntimeError):
@@ -70,6 +76,15 @@ def load() -> ctypes.CDLL:
     lib.hexkv_attend_workspace_bytes.argtypes = [ctypes.POINTER(AttendParams)]
     lib.hexkv_attend.restype = ci
     lib.hexkv_attend.argtypes = [ctypes.POINTER(AttendParams), vp, ctypes.c_size_t, vp]
+    u64 = ctypes.c_uint64
+    lib.hexkv_ipc_export.restype = ci
+    lib.hexkv_ipc_export.argtypes = [vp, ctypes.POINTER(IpcHandle), ctypes.POINTER(u64), ctypes.POINTER(u64)]
+    lib.hexkv_ipc_open.restype = ci
+    lib.hexkv_ipc_open.argtypes = [ctypes.POINTER(IpcHandle), ctypes.POINTER(vp)]
+    lib.hexkv_ipc_close.restype = ci
+    lib.hexkv_ipc_close.argtypes = [vp]
+    lib.hexkv_ipc_dlpack.restype = vp
+    lib.hexkv_ipc_dlpack.argtypes = [vp, u64, ci, ctypes.POINTER(i64), ci, ci, ci]
     _lib = lib
     return lib
 

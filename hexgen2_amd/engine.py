@@ -16,6 +16,10 @@ same validation errors.  What changes is where the bytes go:
 """
 from __future__ import annotations
 
+import hashlib
+import json
+from pathlib import Path
+
 import torch
 
 from . import ops
@@ -23,11 +27,28 @@ from .generation import CacheState
 from .llama import LlamaHost, LlamaShape, read_config
 
 
+# Packed handoff buffers at or above this size are allocated per layer, so
+# that each stays an allocation another process can map (below 2 GiB).
+PER_LAYER_HANDOFF_BYTES = 1 << 30
+
+
+def model_identity(model_dir) -> dict:
+    """SHA-256 of every checkpoint/config file and of their listing, as the
+    pilot records it (hexgen2/record.py:36-45)."""
+    files = sorted(p for p in Path(model_dir).iterdir() if p.is_file() and (
+        p.suffix in {".safetensors", ".json"} or p.name == "tokenizer.model"))
+    hashes = {p.name: hashlib.sha256(p.read_bytes()).hexdigest() for p in files}
+    if not any(name.endswith(".safetensors") for name in hashes):
+        raise ValueError("No safetensors checkpoint in model directory")
+    return {"files": hashes, "sha256": hashlib.sha256(json.dumps(hashes, sort_keys=True).encode()).hexdigest()}
+
+
 class Engine:
     def __init__(self, model_dir, engine="native", device="cuda", dtype="float16",
                  fused_append: bool = False):
         self.device, self.dtype = torch.device(device), getattr(torch, dtype)
         self.shape = LlamaShape.from_config(read_config(model_dir))
+        self.identity = model_identity(model_dir)
         self.kind = engine
         if engine != "native":
             raise ValueError("Only the native engine runs on the hexkv data path; the "
@@ -50,8 +71,16 @@ class Engine:
         n_layers = len(state.key_value_memory_dict)
         layers = [state.key_value_memory_dict[i] for i in range(n_layers)]
         # Send only initialized prompt positions, never the unused capacity:
-        # one launch gathers every layer into one handoff buffer.
-        packed = ops.pack_live(layers, [len(input_ids)])
+        # one launch gathers every layer into one handoff buffer (per-layer
+        # buffers when it would be too large to map from another process).
+        row_shape = layers[0].shape[2:]
+        nbytes = n_layers * len(input_ids) * layers[0][0, 0].numel() * layers[0].element_size()
+        if nbytes >= PER_LAYER_HANDOFF_BYTES:
+            out = [torch.empty((len(input_ids), *row_shape), dtype=self.dtype, device=self.device)
+                   for _ in range(n_layers)]
+            packed = ops.pack_live(layers, [len(input_ids)], out=out)
+        else:
+            packed = ops.pack_live(layers, [len(input_ids)])
         cache = {i: packed[i].unsqueeze(0) for i in range(n_layers)}
         return logits.argmax(-1), cache, logits
 

@@ -2,14 +2,19 @@
 
 Same entry points, header format and validation as the pilot's transport
 (hexgen2/transport.py:13-100): ``validate_header``, ``send_packet``,
-``recv_packet``, ``send_data``, ``recv_data``.  Two carriers:
+``recv_packet``, ``send_data``, ``recv_data``.  Three carriers:
 
-* ``DeviceChannel`` -- prefill and decode on the same GPU: the header is
-  encoded, size-checked and parsed exactly as on the wire, and the tensors
-  are handed over in device memory (no copy, no host round trip).  This is
-  the carrier of the KV handoff in this build.  The receiver gets the
-  sender's (contiguous) tensors; the sender must not modify them after
-  sending, which the pilot never does (run.py:146-177).
+* ``DeviceChannel`` -- prefill and decode in one process on the same GPU:
+  the header is encoded, size-checked and parsed exactly as on the wire, and
+  the tensors are handed over in device memory (no copy, no host round
+  trip).  The receiver gets the sender's (contiguous) tensors; the sender
+  must not modify them after sending, which the pilot never does
+  (run.py:146-177).
+* ``IpcChannel`` -- prefill and decode in two processes on the same GPU:
+  the header plus one IPC descriptor per tensor travel over
+  ``torch.distributed`` (a host group, e.g. Gloo), the bytes stay where the
+  sender's kernels wrote them and the receiver reads them through a mapping
+  of the sender's allocation (``hexkv_ipc_*`` in libhexkv).
 * ``torch.distributed`` -- when no channel is active, packets use the
   reference's wire protocol (int64 header length, UTF-8 JSON header, then one
   send per non-empty tensor in header order), so a peer running the
@@ -22,10 +27,12 @@ from __future__ import annotations
 
 import collections
 import contextlib
+import ctypes
 import json
 import math
+import struct
 import threading
-from typing import Optional
+from typing import Optional, Union
 
 import torch
 import torch.distributed as dist
@@ -133,11 +140,119 @@ class DeviceChannel:
         return tensors, header["metadata"]
 
 
+# DLPack (v0.8) type codes of the packet dtypes: (code, bits).
+_DLPACK = {torch.float16: (2, 16), torch.bfloat16: (4, 16), torch.float32: (2, 32),
+           torch.float64: (2, 64), torch.int64: (0, 64), torch.int32: (0, 32),
+           torch.int16: (0, 16), torch.int8: (0, 8), torch.uint8: (1, 8), torch.bool: (6, 8)}
+_DESCRIPTOR = struct.Struct("<64sQQ")  # IPC handle, byte offset in the allocation, allocation bytes
+IPC_ALLOCATION_LIMIT = 2 * 1024 ** 3  # mapped allocations must stay below 2 GiB on this platform
+_CAPSULE_NAME = b"dltensor"
+_capsule_new = ctypes.pythonapi.PyCapsule_New
+_capsule_new.restype = ctypes.py_object
+_capsule_new.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
+
+
+class IpcChannel:
+    """Packets between two processes that share one GPU.
+
+    ``send`` encodes and validates the header exactly as the wire does, makes
+    every tensor contiguous on the device, synchronises the sender's stream so
+    the bytes are complete, and sends over ``torch.distributed`` (``group``;
+    host tensors only): the int64 header length, the header, then one
+    80-byte descriptor per tensor (IPC handle of the allocation holding it,
+    byte offset, allocation size).  ``recv`` maps the allocations and returns
+    tensors that alias the sender's memory (zero-size tensors are created
+    locally).
+
+    Lifetime protocol: the sender keeps every tensor of a packet alive until
+    it next receives a packet from that peer; the receiver must drop the
+    tensors of a packet (which unmaps them) before it sends to that peer
+    again.  The prefill/decode request cycle (send KV, reply with tokens)
+    follows it.
+    """
+
+    def __init__(self, group=None, max_payload: Optional[int] = None):
+        self.group = group
+        self.max_payload = max_payload if max_payload is not None else 1 << 62
+        self._held = collections.defaultdict(list)
+
+    def send(self, tensors, metadata, dst: int) -> int:
+        from . import _lib
+        encoded, payload = _encode_header(tensors, metadata, self.max_payload)
+        lib = _lib.load()
+        items, descriptors = [], bytearray()
+        for name, tensor in tensors.items():
+            tensor = tensor.detach()
+            if not tensor.is_cuda:
+                raise ValueError(f"IPC packets carry device tensors; {name!r} is on {tensor.device}")
+            tensor = tensor.contiguous()
+            items.append(tensor)
+            if tensor.numel() == 0:
+                descriptors += _DESCRIPTOR.pack(bytes(64), 0, 0)
+                continue
+            handle, offset, size = _lib.IpcHandle(), ctypes.c_uint64(), ctypes.c_uint64()
+            _lib.check(lib.hexkv_ipc_export(tensor.data_ptr(), ctypes.byref(handle), ctypes.byref(offset),
+                                            ctypes.byref(size)), "hexkv_ipc_export")
+            if size.value >= IPC_ALLOCATION_LIMIT:
+                raise ValueError(f"tensor {name!r} lives in a {size.value}-byte allocation; IPC handoff "
+                                 "needs allocations below 2 GiB (send it in per-layer tensors)")
+            descriptors += _DESCRIPTOR.pack(bytes(handle.bytes), offset.value, size.value)
+        torch.cuda.current_stream().synchronize()
+        dist.send(torch.tensor([len(encoded)], dtype=torch.int64), dst=dst, group=self.group)
+        dist.send(torch.frombuffer(bytearray(encoded), dtype=torch.uint8), dst=dst, group=self.group)
+        dist.send(torch.frombuffer(descriptors, dtype=torch.uint8), dst=dst, group=self.group)
+        self._held[dst].append(items)
+        return payload
+
+    def recv(self, src: int):
+        from . import _lib
+        self._held[src].clear()  # the peer has dropped our earlier packets
+        length = torch.empty(1, dtype=torch.int64)
+        dist.recv(length, src=src, group=self.group)
+        size = int(length.item())
+        if not 0 < size <= MAX_HEADER:
+            raise ValueError("Invalid tensor header length")
+        encoded = torch.empty(size, dtype=torch.uint8)
+        dist.recv(encoded, src=src, group=self.group)
+        header = _decode_header(bytes(encoded.numpy().tobytes()), self.max_payload)
+        descriptors = torch.empty(_DESCRIPTOR.size * len(header["tensors"]), dtype=torch.uint8)
+        dist.recv(descriptors, src=src, group=self.group)
+        raw = descriptors.numpy().tobytes()
+        lib = _lib.load()
+        device = torch.cuda.current_device()
+        tensors = {}
+        for i, item in enumerate(header["tensors"]):
+            handle_bytes, offset, alloc = _DESCRIPTOR.unpack_from(raw, i * _DESCRIPTOR.size)
+            dtype, shape = DTYPES[item["dtype"]], item["shape"]
+            nbytes = math.prod(shape) * _ELEMENT_BYTES[item["dtype"]]
+            if nbytes == 0:
+                tensors[item["name"]] = torch.empty(shape, dtype=dtype, device=device)
+                continue
+            if offset + nbytes > alloc:
+                raise ValueError("IPC descriptor does not cover the tensor its header names")
+            handle = _lib.IpcHandle()
+            ctypes.memmove(handle.bytes, handle_bytes, 64)
+            base = ctypes.c_void_p()
+            _lib.check(lib.hexkv_ipc_open(ctypes.byref(handle), ctypes.byref(base)), "hexkv_ipc_open")
+            code, bits = _DLPACK[dtype]
+            dims = (ctypes.c_int64 * max(1, len(shape)))(*shape)
+            managed = lib.hexkv_ipc_dlpack(base, offset, len(shape), dims, code, bits, device)
+            if not managed:
+                lib.hexkv_ipc_close(base)
+                raise ValueError(lib.hexkv_last_error().decode())
+            tensors[item["name"]] = torch.utils.dlpack.from_dlpack(
+                _capsule_new(managed, _CAPSULE_NAME, None))
+        return tensors, header["metadata"]
+
+
 _active = threading.local()
 
 
+Channel = Union[DeviceChannel, IpcChannel]
+
+
 @contextlib.contextmanager
-def use_channel(channel: DeviceChannel):
+def use_channel(channel: Channel):
     """Route send_packet/recv_packet calls in this block through ``channel``."""
     previous = getattr(_active, "channel", None)
     _active.channel = channel
@@ -157,7 +272,7 @@ def wire_device():
             else torch.device("cpu"))
 
 
-def send_packet(tensors, metadata, dst, channel: Optional[DeviceChannel] = None):
+def send_packet(tensors, metadata, dst, channel: Optional[Channel] = None):
     """Send named tensors plus JSON metadata to ``dst``; returns payload bytes."""
     channel = _channel(channel)
     if channel is not None:
@@ -173,7 +288,7 @@ def send_packet(tensors, metadata, dst, channel: Optional[DeviceChannel] = None)
     return payload_bytes
 
 
-def recv_packet(src, channel: Optional[DeviceChannel] = None):
+def recv_packet(src, channel: Optional[Channel] = None):
     """Receive one packet from ``src``; returns (dict of tensors, metadata)."""
     channel = _channel(channel)
     if channel is not None:
@@ -196,7 +311,7 @@ def recv_packet(src, channel: Optional[DeviceChannel] = None):
     return tensors, header["metadata"]
 
 
-def send_data(single_tensor, tensor_dict, dst, channel: Optional[DeviceChannel] = None):
+def send_data(single_tensor, tensor_dict, dst, channel: Optional[Channel] = None):
     """Legacy API: a token tensor plus a KV dict keyed by int layer
     (hexgen2/transport.py:83-90)."""
     keys = list(tensor_dict)
@@ -206,7 +321,7 @@ def send_data(single_tensor, tensor_dict, dst, channel: Optional[DeviceChannel] 
                        {"layers": keys}, dst, channel=channel)
 
 
-def recv_data(src, num_layers=None, tensor_shape=None, channel: Optional[DeviceChannel] = None):
+def recv_data(src, num_layers=None, tensor_shape=None, channel: Optional[Channel] = None):
     """Legacy API counterpart of ``send_data`` (hexgen2/transport.py:93-100)."""
     tensors, metadata = recv_packet(src, channel=channel)
     cache = {key: tensors[f"kv/{key}"] for key in metadata["layers"]}

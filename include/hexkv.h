@@ -193,6 +193,45 @@ size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p);
 int hexkv_attend(const hexkv_attend_params *p, void *workspace,
                  size_t workspace_bytes, hexkv_stream_t stream);
 
+/*
+ * Cross-process handoff on one GPU.  Two processes sharing the GPU (the
+ * prefill and decode ranks of the pilot, hexgen2/run.py:141-198) hand the
+ * packed KV buffer over in device memory: the sender exports an IPC handle of
+ * the allocation holding each tensor, the handle and offset travel in the
+ * packet header's host message, and the receiver maps the allocation and
+ * reads the bytes where they lie.  These calls replace the payload leg of
+ * send_packet/recv_packet (hexgen2/transport.py:56-59, 75-78); the header
+ * leg is unchanged.
+ *
+ * The mapped allocation must stay alive in the sender until the receiver has
+ * closed every mapping of it.  On this platform an exported allocation must
+ * be smaller than 2 GiB.
+ */
+typedef struct hexkv_ipc_handle {
+  unsigned char bytes[64];
+} hexkv_ipc_handle;
+
+/* Handle of the device allocation containing `ptr`, the byte offset of `ptr`
+ * in it, and the allocation's size. */
+int hexkv_ipc_export(const void *ptr, hexkv_ipc_handle *handle, uint64_t *offset,
+                     uint64_t *alloc_bytes);
+
+/* Maps an exported allocation into this process (or takes one more reference
+ * to an existing mapping of the same handle); *base is its first byte. */
+int hexkv_ipc_open(const hexkv_ipc_handle *handle, void **base);
+
+/* Drops one reference to a mapping; the last one synchronises the device (no
+ * enqueued work may still read it) and unmaps it. */
+int hexkv_ipc_close(void *base);
+
+/* A DLPack (v0.8 `DLManagedTensor`, device kDLROCM) view of `ndim`-dimensional
+ * compact row-major data at base + offset, for a framework's from_dlpack.  It
+ * takes over one reference of the mapping from hexkv_ipc_open: the view's
+ * deleter closes it.  dtype_code/bits follow DLPack (kDLInt 0, kDLUInt 1,
+ * kDLFloat 2, kDLBfloat 4, kDLBool 6).  Returns NULL on bad arguments. */
+void *hexkv_ipc_dlpack(void *base, uint64_t offset, int ndim, const int64_t *shape,
+                       int dtype_code, int dtype_bits, int device_id);
+
 #ifdef __cplusplus
 }
 #endif

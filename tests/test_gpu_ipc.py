@@ -1,0 +1,71 @@
+"""Two processes on one GPU exchanging packets through IpcChannel: header over
+Gloo, bytes read from the sender's device memory through an IPC mapping.
+
+Checks bit-exact delivery of the reference's transport fixture values
+(non-contiguous and constant layers, three dtypes, layer order [7, 2]) and of
+random packed KV layers, zero-size tensors, the lifetime protocol (the
+sender's packet survives until the reply) and header validation."""
+import os
+from datetime import timedelta
+from pathlib import Path
+
+import pytest
+import torch
+import torch.distributed as dist
+import torch.multiprocessing as mp
+
+pytestmark = pytest.mark.gpu
+
+
+def _worker(rank, rendezvous):
+    from hexgen2_amd.transport import IpcChannel, recv_data, recv_packet, send_data, send_packet
+    torch.cuda.set_device(0)
+    dist.init_process_group("gloo", rank=rank, world_size=2, init_method=Path(rendezvous).as_uri(),
+                            timeout=timedelta(seconds=60))
+    channel = IpcChannel()
+    try:
+        g = torch.Generator(device="cuda").manual_seed(5)
+        for round_, dtype in enumerate((torch.float16, torch.bfloat16, torch.float32)):
+            cache = {7: torch.arange(-24, 24).reshape(1, 4, 2, 2, 3).to(dtype)[..., ::2].cuda(),
+                     2: torch.full((1, 3, 2, 1, 4), -1.25, dtype=dtype, device="cuda")}
+            token = torch.tensor([42, 17], dtype=torch.long, device="cuda")
+            big = torch.randn((3, 1000, 2, 8, 128), generator=g, device="cuda").to(dtype)
+            if rank == 0:
+                send_data(token, cache, dst=1, channel=channel)
+                send_packet({"big": big, "empty": torch.zeros((0, 5), device="cuda")}, {"round": round_}, dst=1,
+                            channel=channel)
+                # the peer checks the bytes against this copy sent by value
+                dist.send(big.cpu(), dst=1)
+                received, returned = recv_data(src=1, num_layers=2, channel=channel)
+                assert received.tolist() == [42, 17] and list(returned) == [7, 2]
+                for key in cache:
+                    assert torch.equal(returned[key].cpu(), cache[key].cpu()), key
+                del received, returned
+            else:
+                received, returned = recv_data(src=0, num_layers=2, channel=channel)
+                tensors, meta = recv_packet(src=0, channel=channel)
+                expect = torch.empty((3, 1000, 2, 8, 128), dtype=dtype)
+                dist.recv(expect, src=0)
+                assert meta == {"round": round_}
+                assert tensors["empty"].shape == (0, 5) and tensors["empty"].is_cuda
+                assert tensors["big"].is_cuda and tensors["big"].dtype == dtype
+                assert torch.equal(tensors["big"].cpu().view(torch.uint8), expect.view(torch.uint8))
+                # read the peer's bytes with a kernel of this process too
+                assert torch.equal((tensors["big"].float() * 2).cpu(), expect.float() * 2)
+                copy_token, copy_cache = received.clone(), {k: v.clone() for k, v in returned.items()}
+                del received, returned, tensors
+                send_data(copy_token, copy_cache, dst=0, channel=channel)
+        dist.barrier()
+    finally:
+        dist.destroy_process_group()
+
+
+def test_ipc_packets_between_two_processes_on_one_gpu(tmp_path):
+    os.environ.setdefault("HSA_ENABLE_IPC_MODE_LEGACY", "0")
+    mp.spawn(_worker, args=(str(tmp_path / "rendezvous"),), nprocs=2, join=True)
+
+
+def test_ipc_rejects_host_tensors(device):
+    from hexgen2_amd.transport import IpcChannel
+    with pytest.raises(ValueError, match="device tensors"):
+        IpcChannel().send({"x": torch.zeros(3)}, {}, dst=1)

@@ -63,7 +63,29 @@ class Job:
         self.plan = ops.AttendPlan(self.q[0], self.decode_layers[0], self.out,
                                    max_seqlens=[self.max_len + t + 1 for t in range(w.decode_steps)],
                                    seqlens=self.seqlens, kv_new=self.kv_new[0])
+        self.positions = self.seqlens.clone()
+        self.graph = None
         torch.cuda.synchronize()
+
+    def capture_graph(self):
+        """The 32-layer decode step as one HIP graph (after an eager pass)."""
+        w = self.w
+        self.graph = ops.DecodeStepGraph(list(self.q.unbind(0)), self.decode_layers, [self.out] * w.layers,
+                                         list(self.kv_new.unbind(0)), self.positions,
+                                         self.max_len + w.decode_steps)
+
+    def run_graph(self, events):
+        """pack -> unpack -> decode steps replayed from the captured graph."""
+        w, ev = self.w, events
+        ev[0].record()
+        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
+        ev[1].record()
+        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        self.positions.copy_(self.seqlens)
+        ev[2].record()
+        for t in range(w.decode_steps):
+            self.graph.replay()
+            ev[3 + t].record()
 
     def run(self, events=None):
         """pack -> unpack -> decode steps; records (pack, unpack, step...) events."""
@@ -255,6 +277,15 @@ def main():
         },
         "cpu_baseline": None,
     }
+    # Secondary figure, outside the timed steps: the same job with each decode
+    # step replayed from one captured HIP graph.
+    job.capture_graph()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    job.run_graph(ev)
+    torch.cuda.synchronize()
+    graph_ms = sum(ev[2 + t].elapsed_time(ev[3 + t]) for t in range(w.decode_steps))
+    result["decode_graph_us_per_step"] = round(graph_ms / w.decode_steps * 1e3, 1)
+    log(f"graph decode {graph_ms:.1f} ms")
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(w, job, args.cpu_budget)

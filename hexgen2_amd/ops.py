@@ -256,7 +256,9 @@ class AttendPlan:
     Building the parameter block once and patching only pointers, the length
     bias and ``max_seqlen`` per call keeps host overhead per layer small; the
     workspace is allocated once for the largest ``max_seqlen`` the loop will
-    use.  Arguments as for ``decode_attention``.
+    use.  Each call launches on the current stream (so a call inside
+    ``torch.cuda.graph`` capture is recorded into the graph).  Arguments as
+    for ``decode_attention``; a plan built with ``kv_new`` is called with one.
     """
 
     def __init__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *,
@@ -273,18 +275,65 @@ class AttendPlan:
             need = max(need, int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params))))
         self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
         self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), self.workspace.numel()
-        self.stream = _stream(q)
+        self.device = q.device
+        self.fused = kv_new is not None
         self.shapes = (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype)
 
     def __call__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
                  kv_new: Optional[torch.Tensor], seqlen_bias: int, max_seqlen: int) -> torch.Tensor:
-        if (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype) != self.shapes:
+        if (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype) != self.shapes \
+                or tuple(out.shape) != self.shapes[0] or out.dtype != q.dtype:
             raise ValueError("AttendPlan called with a different geometry")
+        if (kv_new is not None) != self.fused:
+            raise ValueError("AttendPlan built with kv_new must be called with kv_new, and only then")
         p = self.params
         p.q, p.cache, p.out = q.data_ptr(), cache.data_ptr(), out.data_ptr()
         if kv_new is not None:
             p.kv_new = kv_new.data_ptr()
         p.seqlen_bias, p.max_seqlen = int(seqlen_bias), int(max_seqlen)
-        _lib.check(self.lib.hexkv_attend(ctypes.byref(p), self.ws_ptr, self.ws_bytes, self.stream),
+        _lib.check(self.lib.hexkv_attend(ctypes.byref(p), self.ws_ptr, self.ws_bytes, _stream(q)),
                    "hexkv_attend")
         return out
+
+
+class DecodeStepGraph:
+    """One decode step's fused append + attend over every layer, captured once
+    as a HIP graph and replayed per step.
+
+    ``positions`` (device int32 ``[B]``) holds each sequence's cached length.
+    A replay writes ``kv_new[l]`` at ``positions`` in every layer's cache,
+    attends ``positions + 1`` keys with ``q[l]`` into ``out[l]``, then
+    advances ``positions`` by one -- all inside the graph, so the host issues
+    one launch per step instead of two per layer.  ``max_seqlen`` bounds the
+    attended length over every replay (it sizes the grid and workspace).
+    This is the graph-captured decode step of hexgen_core's generation loop
+    (hexgen/hexgen_core/generation.py:354-443) restricted to the KV path.
+
+    The kernels must have run once eagerly in this process before capture
+    (code objects load on first launch).  Graph nodes hold the tensors'
+    addresses: the tensors must stay alive, and be updated in place, for as
+    long as the graph is replayed.
+    """
+
+    def __init__(self, q_layers: TensorList, cache_layers: TensorList, out_layers: TensorList,
+                 kv_new_layers: TensorList, positions: torch.Tensor, max_seqlen: int,
+                 softmax_scale: Optional[float] = None, kernel: str = "auto"):
+        self.q, self.cache = _as_layers(q_layers), _as_layers(cache_layers)
+        self.out, self.kv_new = _as_layers(out_layers), _as_layers(kv_new_layers)
+        if not (len(self.q) == len(self.cache) == len(self.out) == len(self.kv_new)) or not self.q:
+            raise ValueError("one q, cache, out and kv_new tensor per layer")
+        _require_device(positions)
+        if positions.dtype != torch.int32 or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int32 device tensor")
+        self.positions, self.max_seqlen = positions, int(max_seqlen)
+        self.plan = AttendPlan(self.q[0], self.cache[0], self.out[0], max_seqlens=[self.max_seqlen],
+                               seqlens=positions, kv_new=self.kv_new[0], softmax_scale=softmax_scale,
+                               kernel=kernel)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            for l in range(len(self.q)):
+                self.plan(self.q[l], self.cache[l], self.out[l], self.kv_new[l], 0, self.max_seqlen)
+            self.positions.add_(1)
+
+    def replay(self) -> None:
+        self.graph.replay()

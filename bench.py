@@ -53,7 +53,6 @@ class Job:
             self.prefill[l].normal_(generator=g)
         self.packed = torch.empty((L, w.live_rows, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=device)
         self.decode = torch.empty(shape, dtype=w.dtype, device=device)
-        self.prefill_layers = list(self.prefill.unbind(0))
         self.decode_layers = list(self.decode.unbind(0))
         self.q = torch.randn((L, B, 1, w.q_heads, w.head_dim), generator=g, device=device).to(w.dtype)
         self.kv_new = torch.randn((L, B, 2, w.kv_heads, w.head_dim), generator=g, device=device).to(w.dtype)
@@ -78,9 +77,9 @@ class Job:
         """pack -> unpack -> decode steps replayed from the captured graph."""
         w, ev = self.w, events
         ev[0].record()
-        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
+        ops.pack_live(self.prefill, w.lens, out=self.packed)
         ev[1].record()
-        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        ops.unpack_live(self.packed, self.decode, w.lens)
         self.positions.copy_(self.seqlens)
         ev[2].record()
         for t in range(w.decode_steps):
@@ -93,10 +92,10 @@ class Job:
         ev = events
         if ev is not None:
             ev[0].record()
-        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
+        ops.pack_live(self.prefill, w.lens, out=self.packed)
         if ev is not None:
             ev[1].record()
-        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        ops.unpack_live(self.packed, self.decode, w.lens)
         if ev is not None:
             ev[2].record()
         for t in range(w.decode_steps):
@@ -124,8 +123,8 @@ class Job:
         torch.cuda.synchronize()
         del src, dst
         log("pack, unpack, one decode step")
-        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
-        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        ops.pack_live(self.prefill, w.lens, out=self.packed)
+        ops.unpack_live(self.packed, self.decode, w.lens)
         for l in range(w.layers):
             self.plan(self.q[l], self.decode_layers[l], self.out, self.kv_new[l], 0, self.max_len + 1)
         torch.cuda.synchronize()
@@ -136,14 +135,71 @@ class Job:
         rows equal the prefill cache's (before any append) and the packed
         buffer is the concatenation of live rows; checked on the device."""
         w = self.w
-        ops.pack_live(self.prefill_layers, w.lens, out=self.packed)
-        ops.unpack_live(self.packed, self.decode_layers, w.lens)
+        ops.pack_live(self.prefill, w.lens, out=self.packed)
+        ops.unpack_live(self.packed, self.decode, w.lens)
         start = 0
         for b, n in enumerate(w.lens):
             a = self.prefill[:, b, :n]
             if not torch.equal(a, self.decode[:, b, :n]) or not torch.equal(a, self.packed[:, start:start + n]):
                 raise AssertionError(f"pack/unpack round trip differs for sequence {b}")
             start += n
+
+
+def measure_formats(device, reps=5):
+    """Secondary figures, outside the timed steps: the legacy KV formats
+    (hexgen2_amd.kv_formats) on Llama-shaped synthetic data, each GB/s of
+    algorithmic bytes (bytes read + bytes written, zero padding included):
+
+    * flat packet: 32 layers of one request's live [1, 8192, 2, 8, 128] bf16
+      slice of an 8448-position cache, flattened and concatenated;
+    * zero-pad batching: 8 requests of lengths U[128, 4096] (seed 0), 32
+      layers of [1, L_i, 2, 8, 128] bf16, padded to the longest and stacked;
+    * TP head concat: 16 layers of 8 tensor-parallel shards [8, 4096, 2, 1,
+      128] bf16 (Llama-2-70B's KV heads over TP 8) joined into one
+      [8, 4096, 2, 8, 128] cache per layer.
+    """
+    from hexgen2_amd import kv_formats as kvf
+
+    g = torch.Generator(device=device).manual_seed(3)
+    row = 2 * 8 * 128 * 2
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        for _ in range(reps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]) / reps
+
+    def entry(nbytes, ms):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "ms": round(ms, 4),
+                "bytes": int(nbytes)}
+
+    out = {}
+    cache = torch.empty((32, 1, 8448, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
+    layers = [cache[l, :, :8192] for l in range(32)]
+    flat = torch.empty(32 * 8192 * row // 2, dtype=torch.bfloat16, device=device)
+    out["flat_packet"] = entry(2 * 32 * 8192 * row, timed(lambda: kvf.flat_concat(layers, out=flat)))
+    del cache, layers, flat
+
+    lens = [int(x) for x in torch.randint(128, 4097, (8,), generator=torch.Generator().manual_seed(0))]
+    cache = torch.empty((32, 8, 4096, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
+    dicts = [{l: cache[l, i:i + 1, :n] for l in range(32)} for i, n in enumerate(lens)]
+    nbytes = 32 * row * (sum(lens) + 8 * max(lens))
+    out["zero_pad_batch"] = entry(nbytes, timed(lambda: kvf.batch_key_value_memory_dicts(dicts)))
+    out["zero_pad_batch"]["lens"] = lens
+    del cache, dicts
+
+    shards_t = torch.empty((8, 16, 8, 4096, 2, 1, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
+    shards = [{l: shards_t[j, l] for l in range(16)} for j in range(8)]
+    out["tp_head_concat"] = entry(2 * shards_t.numel() * 2, timed(lambda: kvf.concat_dicts(shards)))
+    del shards_t, shards
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(w, job, budget_s):
@@ -190,6 +246,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--no-formats", action="store_true", help="skip the legacy-format figures")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the short dispatch sequence for hardware-counter runs")
     args = ap.parse_args()
@@ -289,6 +346,11 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(w, job, args.cpu_budget)
+    if not args.no_formats:
+        del job
+        torch.cuda.empty_cache()
+        result["formats"] = measure_formats(device)
+        log(f"legacy formats {result['formats']}")
     print(json.dumps(result), flush=True)
 
 

@@ -19,8 +19,9 @@ MAX_SEQS_PER_LAUNCH = 256
 
 # Every symbol the header declares; tests check the library exports them all.
 EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "hexkv_append",
-           "hexkv_attend_workspace_bytes", "hexkv_attend", "hexkv_ipc_export", "hexkv_ipc_open",
-           "hexkv_ipc_close", "hexkv_ipc_dlpack")
+           "hexkv_attend_workspace_bytes", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
+           "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
+           "hexkv_ipc_dlpack")
 
 
 class AttendParams(ctypes.Structure):
@@ -37,6 +38,12 @@ class AttendParams(ctypes.Structure):
         ("seqlens_dev", ctypes.c_void_p), ("seqlen_bias", ctypes.c_int32), ("max_seqlen", ctypes.c_int32),
         ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int), ("kernel", ctypes.c_int),
     ]
+
+
+class Block(ctypes.Structure):
+    """Mirror of ``hexkv_block``: depth x height rows of ``width`` bytes."""
+    _fields_ = [("data", ctypes.c_void_p), ("width", ctypes.c_int64), ("height", ctypes.c_int64),
+                ("depth", ctypes.c_int64), ("row_pitch", ctypes.c_int64), ("slice_pitch", ctypes.c_int64)]
 
 
 class IpcHandle(ctypes.Structure):
@@ -76,6 +83,13 @@ def load() -> ctypes.CDLL:
     lib.hexkv_attend_workspace_bytes.argtypes = [ctypes.POINTER(AttendParams)]
     lib.hexkv_attend.restype = ci
     lib.hexkv_attend.argtypes = [ctypes.POINTER(AttendParams), vp, ctypes.c_size_t, vp]
+    blocks = ctypes.POINTER(Block)
+    lib.hexkv_flat_concat.restype = ci
+    lib.hexkv_flat_concat.argtypes = [blocks, ci, vp, vp]
+    lib.hexkv_batch_pad.restype = ci
+    lib.hexkv_batch_pad.argtypes = [blocks, ci, ci, ptrs, i64, vp]
+    lib.hexkv_head_concat.restype = ci
+    lib.hexkv_head_concat.argtypes = [blocks, ci, ci, ptrs, vp]
     u64 = ctypes.c_uint64
     lib.hexkv_ipc_export.restype = ci
     lib.hexkv_ipc_export.argtypes = [vp, ctypes.POINTER(IpcHandle), ctypes.POINTER(u64), ctypes.POINTER(u64)]

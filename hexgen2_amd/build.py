@@ -24,7 +24,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INCLUDE}", f"-I{CSRC}",
           "-Wall", "-Wno-unused-function"]
-SOURCES = ["hexkv_status.cpp", "hexkv_copy.hip", "hexkv_attend.hip", "hexkv_ipc.cpp"]
+SOURCES = ["hexkv_status.cpp", "hexkv_copy.hip", "hexkv_attend.hip", "hexkv_blocks.hip", "hexkv_ipc.cpp"]
 
 
 def _compile(source: str) -> Path:

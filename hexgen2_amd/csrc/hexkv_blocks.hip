@@ -1,0 +1,362 @@
+// Strided byte-row gathers of the legacy KV formats: hexkv_flat_concat,
+// hexkv_batch_pad and hexkv_head_concat (hexkv.h).
+//
+// All three reduce to one engine.  A launch carries up to kMaxSpans spans in
+// its kernel arguments; a span is depth x height rows of `width` bytes to
+// move from a source block (or to zero-fill) to a destination with pitches
+// of its own.  The host normalises each span (rows contiguous on both sides
+// merge into one long row; slices that follow each other become rows) and
+// cuts it into tiles of about one chunk of bytes: whole rows when rows are
+// short, row pieces when they are long.  One workgroup moves one tile with
+// nontemporal 16-byte loads and stores (narrower vectors only when an
+// address, pitch or width is not a multiple of 16), four in flight per lane;
+// short rows are spread over the workgroup several per pass, so a 256-byte
+// head slice keeps every lane busy.  The tile -> span lookup is one scalar
+// binary search over the prefix sums of tile counts.
+#include "hexkv_common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace hexkv {
+
+constexpr int kSpanThreads = 256;
+constexpr int kSpanUnroll = 4;
+constexpr int kMaxSpans = 32;
+
+struct Span {
+  const char *src;  // nullptr: zero-fill the destination rows
+  char *dst;
+  int64_t width;                                   // bytes per row
+  int64_t src_row, src_slice, dst_row, dst_slice;  // pitches, bytes
+  int64_t tile_cols;                               // bytes of one row per tile
+  int32_t height;                                  // rows per slice
+  int32_t tile_rows;                               // rows per tile
+  int32_t row_tiles;                               // tiles down one slice
+  int32_t col_tiles;                               // tiles along one row
+};
+
+struct SpanArgs {
+  Span span[kMaxSpans];
+  int32_t first_tile[kMaxSpans + 1];  // prefix sums of tiles per span
+  int32_t n;
+};
+static_assert(sizeof(SpanArgs) <= 4096, "kernel arguments above 4 KiB");
+
+// A wide row piece: the workgroup strides along it.
+template <typename V>
+__device__ __forceinline__ void move_row(const char *__restrict__ s, char *__restrict__ d, int64_t nv) {
+  const V *sv = reinterpret_cast<const V *>(s);
+  V *dv = reinterpret_cast<V *>(d);
+  int64_t i = threadIdx.x;
+  for (; i + (kSpanUnroll - 1) * kSpanThreads < nv; i += kSpanUnroll * kSpanThreads) {
+    V r[kSpanUnroll];
+#pragma unroll
+    for (int u = 0; u < kSpanUnroll; ++u)
+      r[u] = sv ? __builtin_nontemporal_load(sv + i + u * kSpanThreads) : V{};
+#pragma unroll
+    for (int u = 0; u < kSpanUnroll; ++u) __builtin_nontemporal_store(r[u], dv + i + u * kSpanThreads);
+  }
+  for (; i < nv; i += kSpanThreads) __builtin_nontemporal_store(sv ? __builtin_nontemporal_load(sv + i) : V{}, dv + i);
+}
+
+template <typename V>
+__global__ __launch_bounds__(kSpanThreads) void span_copy_kernel(const SpanArgs a) {
+  const int tile = blockIdx.x;
+  int lo = 0, hi = a.n;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (a.first_tile[mid] <= tile) lo = mid; else hi = mid;
+  }
+  const Span &s = a.span[lo];
+  int t = tile - a.first_tile[lo];
+  const int ct = t % s.col_tiles;
+  t /= s.col_tiles;
+  const int rt = t % s.row_tiles;
+  const int64_t k = t / s.row_tiles;  // slice
+  const int r0 = rt * s.tile_rows;
+  const int r1 = min(s.height, r0 + s.tile_rows);
+  const int64_t c0 = static_cast<int64_t>(ct) * s.tile_cols;
+  const int64_t nv = (min(s.width, c0 + s.tile_cols) - c0) / static_cast<int64_t>(sizeof(V));
+  const char *src = s.src ? s.src + k * s.src_slice + c0 : nullptr;
+  char *dst = s.dst + k * s.dst_slice + c0;
+  if (nv >= kSpanThreads) {
+    for (int r = r0; r < r1; ++r)
+      move_row<V>(src ? src + r * s.src_row : nullptr, dst + r * s.dst_row, nv);
+    return;
+  }
+  // Short rows: `per` rows per pass, lane (tr, tc) = (row in pass, vector).
+  const int per = kSpanThreads / static_cast<int>(nv);
+  const int tr = threadIdx.x / static_cast<int>(nv);
+  const int tc = threadIdx.x - tr * static_cast<int>(nv);
+  if (tr >= per) return;
+  const int64_t col = static_cast<int64_t>(tc) * static_cast<int64_t>(sizeof(V));
+  for (int r = r0 + tr; r < r1; r += per * kSpanUnroll) {
+    V v[kSpanUnroll];
+#pragma unroll
+    for (int u = 0; u < kSpanUnroll; ++u) {
+      const int rr = r + u * per;
+      v[u] = V{};
+      if (src && rr < r1) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V *>(src + rr * s.src_row + col));
+    }
+#pragma unroll
+    for (int u = 0; u < kSpanUnroll; ++u) {
+      const int rr = r + u * per;
+      if (rr < r1) __builtin_nontemporal_store(v[u], reinterpret_cast<V *>(dst + rr * s.dst_row + col));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host ---
+
+// One span before tiling (all sizes in bytes).
+struct Move {
+  const char *src;  // nullptr: zero fill
+  char *dst;
+  int64_t width, height, depth;
+  int64_t src_row, src_slice, dst_row, dst_slice;
+};
+
+static int64_t move_bytes(const Move &m) { return m.width * m.height * m.depth; }
+
+// Merges dimensions that are contiguous on both sides, so the engine moves
+// the longest possible rows and tiles several short rows together.
+static void normalise(Move &m) {
+  auto merge_rows = [&m] {  // rows follow each other on both sides: one row
+    if (m.height > 1 && m.dst_row == m.width && (!m.src || m.src_row == m.width)) {
+      m.width *= m.height;
+      m.height = 1;
+      m.src_row = m.dst_row = m.width;
+    }
+  };
+  merge_rows();
+  if (m.depth > 1 && m.dst_slice == m.height * m.dst_row && (!m.src || m.src_slice == m.height * m.src_row)) {
+    m.height *= m.depth;  // slices follow each other: one slice
+    m.depth = 1;
+  } else if (m.height == 1 && m.depth > 1) {
+    m.height = m.depth;  // single-row slices become rows, so short ones share a tile
+    m.src_row = m.src_slice;
+    m.dst_row = m.dst_slice;
+    m.depth = 1;
+  }
+  merge_rows();
+}
+
+// Bytes per tile: about total / 8192 workgroups, 16 KB to 256 KB.
+static int64_t tile_bytes(int64_t total) {
+  const int64_t chunk = (total / 8192 + 4095) / 4096 * 4096;
+  return std::min<int64_t>(std::max<int64_t>(chunk, 16384), 262144);
+}
+
+template <typename V>
+static void launch_spans(const SpanArgs &a, int tiles, hipStream_t s) {
+  span_copy_kernel<V><<<dim3(static_cast<unsigned>(tiles)), kSpanThreads, 0, s>>>(a);
+}
+
+// Moves every span, kMaxSpans per launch, in order on `stream`.
+static int run_moves(std::vector<Move> &moves, hipStream_t stream, const char *what) {
+  int64_t total = 0;
+  uint64_t align = 0;  // OR of every address, pitch and width in use
+  std::vector<Move> live;
+  live.reserve(moves.size());
+  for (Move &m : moves) {
+    if (move_bytes(m) == 0) continue;
+    normalise(m);
+    if (m.height > INT32_MAX) return fail(HEXKV_ERANGE, "%s: more than 2^31-1 rows in one block", what);
+    total += move_bytes(m);
+    align |= reinterpret_cast<uintptr_t>(m.dst) | static_cast<uint64_t>(m.width);
+    if (m.src) align |= reinterpret_cast<uintptr_t>(m.src);
+    if (m.height > 1) align |= static_cast<uint64_t>(m.dst_row) | static_cast<uint64_t>(m.src ? m.src_row : 0);
+    if (m.depth > 1)
+      align |= static_cast<uint64_t>(m.dst_slice) | static_cast<uint64_t>(m.src ? m.src_slice : 0);
+    live.push_back(m);
+  }
+  if (live.empty()) return HEXKV_OK;
+  const int vec = (align & 15) == 0 ? 16 : (align & 3) == 0 ? 4 : (align & 1) == 0 ? 2 : 1;
+  const int64_t chunk = tile_bytes(total);
+
+  size_t i = 0;
+  while (i < live.size()) {
+    SpanArgs a;
+    int64_t tiles = 0;
+    int n = 0;
+    for (; i < live.size() && n < kMaxSpans; ++i, ++n) {
+      const Move &m = live[i];
+      Span &s = a.span[n];
+      s.src = m.src;
+      s.dst = m.dst;
+      s.width = m.width;
+      s.src_row = m.src_row;
+      s.src_slice = m.src_slice;
+      s.dst_row = m.dst_row;
+      s.dst_slice = m.dst_slice;
+      s.height = static_cast<int32_t>(m.height);
+      int64_t col_tiles, row_tiles, tile_rows;
+      if (m.width >= chunk) {
+        s.tile_cols = chunk;
+        col_tiles = (m.width + chunk - 1) / chunk;
+        tile_rows = 1;
+        row_tiles = m.height;
+      } else {
+        s.tile_cols = m.width;
+        col_tiles = 1;
+        tile_rows = std::max<int64_t>(1, chunk / m.width);
+        row_tiles = (m.height + tile_rows - 1) / tile_rows;
+      }
+      const int64_t span_tiles = m.depth * row_tiles * col_tiles;
+      if (span_tiles > INT32_MAX || tiles + span_tiles > INT32_MAX) {
+        if (n == 0) return fail(HEXKV_ERANGE, "%s: block too large for one launch", what);
+        break;  // next launch
+      }
+      s.tile_rows = static_cast<int32_t>(std::min<int64_t>(tile_rows, m.height));
+      s.row_tiles = static_cast<int32_t>(row_tiles);
+      s.col_tiles = static_cast<int32_t>(col_tiles);
+      a.first_tile[n] = static_cast<int32_t>(tiles);
+      tiles += span_tiles;
+    }
+    a.first_tile[n] = static_cast<int32_t>(tiles);
+    a.n = n;
+    switch (vec) {
+      case 16: launch_spans<u32x4>(a, static_cast<int>(tiles), stream); break;
+      case 4: launch_spans<unsigned int>(a, static_cast<int>(tiles), stream); break;
+      case 2: launch_spans<unsigned short>(a, static_cast<int>(tiles), stream); break;
+      default: launch_spans<unsigned char>(a, static_cast<int>(tiles), stream); break;
+    }
+    const int rc = check_launch(what);
+    if (rc != HEXKV_OK) return rc;
+  }
+  return HEXKV_OK;
+}
+
+// Shape checks shared by the entry points: non-negative sizes, bytes that
+// fit int64, a device address whenever the block holds bytes.
+constexpr int64_t kMaxBytes = INT64_C(1) << 46;  // 64 TiB: no product below overflows
+
+static int check_block(const hexkv_block &b, const char *what, int index) {
+  if (b.width < 0 || b.height < 0 || b.depth < 0)
+    return fail(HEXKV_EINVAL, "%s: block %d has a negative size", what, index);
+  if (b.width == 0 || b.height == 0 || b.depth == 0) return HEXKV_OK;
+  if (b.row_pitch < 0 || b.slice_pitch < 0)
+    return fail(HEXKV_EINVAL, "%s: block %d has a negative pitch", what, index);
+  if (b.width > kMaxBytes || b.height > kMaxBytes || b.depth > kMaxBytes ||
+      b.width * b.height > kMaxBytes || b.width * b.height * b.depth > kMaxBytes)
+    return fail(HEXKV_ERANGE, "%s: block %d is larger than 64 TiB", what, index);
+  if (!b.data) return fail(HEXKV_EINVAL, "%s: block %d has no data pointer", what, index);
+  return HEXKV_OK;
+}
+
+}  // namespace hexkv
+
+extern "C" int hexkv_flat_concat(const hexkv_block *src, int n, void *dst, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_flat_concat";
+  if (n < 0) return fail(HEXKV_EINVAL, "%s: negative block count", what);
+  if (n > 0 && !src) return fail(HEXKV_EINVAL, "%s: null block array", what);
+  std::vector<Move> moves;
+  int64_t off = 0;
+  for (int i = 0; i < n; ++i) {
+    int rc = check_block(src[i], what, i);
+    if (rc != HEXKV_OK) return rc;
+    const hexkv_block &b = src[i];
+    const int64_t bytes = b.width * b.height * b.depth;
+    if (bytes == 0) continue;
+    if (!dst) return fail(HEXKV_EINVAL, "%s: null destination", what);
+    if (off > kMaxBytes) return fail(HEXKV_ERANGE, "%s: concatenation larger than 64 TiB", what);
+    moves.push_back(Move{static_cast<const char *>(b.data), static_cast<char *>(dst) + off, b.width,
+                         b.height, b.depth, b.row_pitch, b.slice_pitch, b.width, b.width * b.height});
+    off += bytes;
+  }
+  return run_moves(moves, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int hexkv_batch_pad(const hexkv_block *src, int n_layers, int n_req, void *const *dst_layers,
+                               int64_t max_rows, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_batch_pad";
+  if (n_layers < 0 || n_req < 0 || max_rows < 0) return fail(HEXKV_EINVAL, "%s: negative count", what);
+  if (n_layers == 0 || n_req == 0) return HEXKV_OK;
+  if (!src || !dst_layers) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  const int64_t width = src[0].width;
+  int64_t seqs = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    for (int i = 0; i < n_req; ++i) {
+      const hexkv_block &b = src[static_cast<int64_t>(l) * n_req + i];
+      int rc = check_block(b, what, l * n_req + i);
+      if (rc != HEXKV_OK) return rc;
+      const hexkv_block &first = src[i];
+      if (b.width != width)
+        return fail(HEXKV_EINVAL, "%s: request %d of layer %d has rows of %lld bytes, not %lld", what, i, l,
+                    static_cast<long long>(b.width), static_cast<long long>(width));
+      if (b.depth != first.depth || b.height != first.height)
+        return fail(HEXKV_EINVAL, "%s: request %d has other sizes in layer %d than in layer 0", what, i, l);
+      if (b.height > max_rows)
+        return fail(HEXKV_ERANGE, "%s: request %d holds %lld rows, above max_rows %lld", what, i,
+                    static_cast<long long>(b.height), static_cast<long long>(max_rows));
+    }
+  }
+  for (int i = 0; i < n_req && seqs <= kMaxBytes; ++i) seqs += src[i].depth;
+  if (width > 0 && max_rows > kMaxBytes / width)
+    return fail(HEXKV_ERANGE, "%s: padded sequence larger than 64 TiB", what);
+  const int64_t seq_bytes = max_rows * width;
+  if (seqs > kMaxBytes || (seq_bytes > 0 && seqs > kMaxBytes / seq_bytes))
+    return fail(HEXKV_ERANGE, "%s: batched layer larger than 64 TiB", what);
+  std::vector<Move> moves;
+  for (int l = 0; l < n_layers; ++l) {
+    if (seqs * seq_bytes == 0) break;
+    if (!dst_layers[l]) return fail(HEXKV_EINVAL, "%s: null destination of layer %d", what, l);
+    char *base = static_cast<char *>(dst_layers[l]);
+    for (int i = 0; i < n_req; ++i) {
+      const hexkv_block &b = src[static_cast<int64_t>(l) * n_req + i];
+      moves.push_back(Move{static_cast<const char *>(b.data), base, width, b.height, b.depth, b.row_pitch,
+                           b.slice_pitch, width, seq_bytes});
+      moves.push_back(Move{nullptr, base + b.height * width, width, max_rows - b.height, b.depth, 0, 0,
+                           width, seq_bytes});
+      base += b.depth * seq_bytes;
+    }
+  }
+  return run_moves(moves, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int hexkv_head_concat(const hexkv_block *src, int n_layers, int n_shards, void *const *dst_layers,
+                                 hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_head_concat";
+  if (n_layers < 0 || n_shards < 0) return fail(HEXKV_EINVAL, "%s: negative count", what);
+  if (n_layers == 0 || n_shards == 0) return HEXKV_OK;
+  if (!src || !dst_layers) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  int64_t row = 0;  // destination row bytes
+  for (int j = 0; j < n_shards; ++j) {
+    if (src[j].width < 0 || src[j].width > kMaxBytes || row > kMaxBytes)
+      return fail(HEXKV_ERANGE, "%s: shard %d row width out of range", what, j);
+    row += src[j].width;
+  }
+  std::vector<Move> moves;
+  for (int l = 0; l < n_layers; ++l) {
+    const hexkv_block *shards = src + static_cast<int64_t>(l) * n_shards;
+    for (int j = 0; j < n_shards; ++j) {
+      int rc = check_block(shards[j], what, l * n_shards + j);
+      if (rc != HEXKV_OK) return rc;
+      if (shards[j].width != src[j].width)
+        return fail(HEXKV_EINVAL, "%s: shard %d of layer %d has rows of %lld bytes, %lld in layer 0", what, j,
+                    l, static_cast<long long>(shards[j].width), static_cast<long long>(src[j].width));
+      if (shards[j].depth * shards[j].height != shards[0].depth * shards[0].height)
+        return fail(HEXKV_EINVAL, "%s: the shards of layer %d hold different numbers of rows", what, l);
+    }
+    const int64_t rows = shards[0].depth * shards[0].height;
+    if (row == 0 || rows == 0) continue;
+    if (row > kMaxBytes / rows) return fail(HEXKV_ERANGE, "%s: concatenated layer larger than 64 TiB", what);
+    if (!dst_layers[l]) return fail(HEXKV_EINVAL, "%s: null destination of layer %d", what, l);
+    int64_t col = 0;
+    for (int j = 0; j < n_shards; ++j) {
+      // Destination row k * height_j + r of shard j's (slice k, row r).
+      const hexkv_block &b = shards[j];
+      moves.push_back(Move{static_cast<const char *>(b.data), static_cast<char *>(dst_layers[l]) + col, b.width,
+                           b.height, b.depth, b.row_pitch, b.slice_pitch, row, row * b.height});
+      col += b.width;
+    }
+  }
+  return run_moves(moves, static_cast<hipStream_t>(stream), what);
+}

@@ -61,8 +61,26 @@ def _check_lens(lens: Sequence[int], batch: int) -> list:
     return lens
 
 
+def _layer_ptrs(stacked: torch.Tensor) -> list:
+    """Base address of each layer of a stacked ``[n_layers, ...]`` tensor."""
+    step = stacked.stride(0) * stacked.element_size()
+    base = stacked.data_ptr()
+    return [base + l * step for l in range(stacked.shape[0])]
+
+
 def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, dtype, device):
-    layers = _as_layers(packed)
+    if isinstance(packed, torch.Tensor):
+        # Stacked [n_layers, total, *row]: checked once, addressed per layer.
+        _require_device(packed)
+        if packed.dtype != dtype or packed.device != device:
+            raise ValueError("packed and cache tensors differ in dtype or device")
+        if packed.dim() < 1 or packed.shape[0] != n_layers:
+            raise ValueError(f"packed tensor of shape {tuple(packed.shape)} for {n_layers} cache layers")
+        if packed[0].numel() != total * row_elems or not packed[0].is_contiguous():
+            raise ValueError(f"packed layer must be contiguous with {total} rows of {row_elems} "
+                             f"elements, got shape {tuple(packed.shape[1:])}")
+        return _layer_ptrs(packed)
+    layers = list(packed)
     if len(layers) != n_layers:
         raise ValueError(f"{len(layers)} packed layers for {n_layers} cache layers")
     ptrs = []
@@ -78,7 +96,16 @@ def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, 
 
 
 def _cache_ptrs(cache_layers: TensorList):
-    layers = _as_layers(cache_layers)
+    """(first layer, per-layer base addresses, row geometry) of the cache
+    layers: a list of ``[B, S, *row]`` tensors sharing shape, strides, dtype
+    and device, or one stacked ``[n_layers, B, S, *row]`` tensor."""
+    if isinstance(cache_layers, torch.Tensor):
+        if cache_layers.dim() < 1 or cache_layers.shape[0] == 0:
+            raise ValueError("no cache layers")
+        _require_device(cache_layers)
+        first = cache_layers[0]
+        return first, _layer_ptrs(cache_layers), _row_geometry(first)
+    layers = list(cache_layers)
     if not layers:
         raise ValueError("no cache layers")
     first = layers[0]
@@ -89,7 +116,7 @@ def _cache_ptrs(cache_layers: TensorList):
         if t.shape != first.shape or t.dtype != first.dtype or t.device != first.device \
                 or t.stride() != first.stride():
             raise ValueError("all cache layers must share shape, strides, dtype and device")
-    return first, layers, geometry
+    return first, [t.data_ptr() for t in layers], geometry
 
 
 def pack_live(cache_layers: TensorList, lens: Sequence[int],
@@ -98,8 +125,10 @@ def pack_live(cache_layers: TensorList, lens: Sequence[int],
     packed handoff layout ``[n_layers, sum(lens), *row]`` (one launch).
 
     Batch-1 form of hexgen2/model.py:81 ``t[:, :L].contiguous()`` per layer,
-    generalised to ragged batches.  ``out`` may be one ``[n_layers, T, *row]``
-    tensor or a list of per-layer contiguous tensors.
+    generalised to ragged batches.  ``cache_layers`` is a list of per-layer
+    ``[B, S, *row]`` caches or one stacked ``[n_layers, B, S, *row]`` tensor
+    (checked once, the cheaper form for many layers); ``out`` may be one
+    ``[n_layers, T, *row]`` tensor or a list of per-layer contiguous tensors.
     """
     first, layers, (row_elems, row_bytes, seq_stride) = _cache_ptrs(cache_layers)
     lens = _check_lens(lens, first.shape[0])
@@ -109,7 +138,7 @@ def pack_live(cache_layers: TensorList, lens: Sequence[int],
                           device=first.device)
     dst = _packed_ptrs(out, len(layers), total, row_elems, first.dtype, first.device)
     n = len(layers)
-    rc = _lib.load().hexkv_pack((ctypes.c_void_p * n)(*[t.data_ptr() for t in layers]),
+    rc = _lib.load().hexkv_pack((ctypes.c_void_p * n)(*layers),
                                 (ctypes.c_void_p * n)(*dst), n, len(lens), seq_stride,
                                 first.shape[1], row_bytes, (ctypes.c_int64 * len(lens))(*lens),
                                 _stream(first))
@@ -126,7 +155,7 @@ def unpack_live(packed: TensorList, cache_layers: TensorList, lens: Sequence[int
     src = _packed_ptrs(packed, len(layers), sum(lens), row_elems, first.dtype, first.device)
     n = len(layers)
     rc = _lib.load().hexkv_unpack((ctypes.c_void_p * n)(*src),
-                                  (ctypes.c_void_p * n)(*[t.data_ptr() for t in layers]), n,
+                                  (ctypes.c_void_p * n)(*layers), n,
                                   len(lens), seq_stride, first.shape[1], row_bytes,
                                   (ctypes.c_int64 * len(lens))(*lens), _stream(first))
     _lib.check(rc, "hexkv_unpack")

@@ -194,6 +194,72 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
                  size_t workspace_bytes, hexkv_stream_t stream);
 
 /*
+ * Legacy KV formats of HexGen's earlier disaggregation scripts
+ * (hexgen/llama/): the flat-concatenated packet, zero-padded request
+ * batching and the tensor-parallel head concatenation.  Each is a strided
+ * gather of byte rows, described by blocks.
+ *
+ * A block is depth x height rows of `width` contiguous bytes at
+ *   data + k * slice_pitch + r * row_pitch      (k < depth, r < height),
+ * e.g. a cache view [B, L, 2, Hkv, D] of one layer is depth = B sequences,
+ * height = L positions, width = one row (2*Hkv*D*elem), row_pitch and
+ * slice_pitch its position and batch strides in bytes.  A block's "compact"
+ * order is slice by slice, row by row.  Sources may alias each other; a
+ * destination must not overlap any source.
+ */
+typedef struct hexkv_block {
+  const void *data;    /* device address of byte 0 of row 0 of slice 0 */
+  int64_t width;       /* contiguous bytes per row                      */
+  int64_t height;      /* rows per slice                                */
+  int64_t depth;       /* slices                                        */
+  int64_t row_pitch;   /* bytes from one row to the next                */
+  int64_t slice_pitch; /* bytes from one slice to the next              */
+} hexkv_block;
+
+/*
+ * Flat concatenation: the bytes of src[0], src[1], ... src[n-1], each in
+ * compact order, laid end to end at dst.
+ *
+ * Replaces the payload build of send_key_value_memory_dict,
+ *   torch.cat([t.flatten() for t in key_value_memory_dict.values()])
+ *   (hexgen/llama/kv_cache_communication.py:21-26); the receiver's per-layer
+ *   tensors are views of the flat buffer (:50-57).
+ */
+int hexkv_flat_concat(const hexkv_block *src, int n, void *dst, hexkv_stream_t stream);
+
+/*
+ * Zero-padded batching: for every layer l < n_layers the requests' caches
+ * src[l * n_req + i] (depth b_i sequences x height len_i positions x width
+ * row bytes) are stacked into dst_layers[l], a contiguous
+ * [sum_i b_i][max_rows][row] buffer, request i's sequences after those of
+ * requests < i; rows [len_i, max_rows) of each of its sequences are zero.
+ * b_i and len_i of request i must agree over layers, the width over all
+ * blocks, and len_i <= max_rows.
+ *
+ * Replaces the per-layer F.pad + torch.cat of
+ * batch_logits_and_key_value_memory_dict (hexgen/llama/kv_cache_batch.py:
+ * 4-28) with max_rows = max_i len_i.
+ */
+int hexkv_batch_pad(const hexkv_block *src, int n_layers, int n_req, void *const *dst_layers,
+                    int64_t max_rows, hexkv_stream_t stream);
+
+/*
+ * Head concatenation of tensor-parallel shards: for every layer l the
+ * shards src[l * n_shards + j] (depth x height rows of w_j bytes, one row =
+ * one (sequence, position, K|V) slice of shard j's heads, rows numbered
+ * slice by slice) are joined row by row into dst_layers[l], a contiguous
+ * [rows][sum_j w_j] buffer, shard j at byte column w_0 + ... + w_{j-1}.  The
+ * row count depth x height must agree over a layer's shards, w_j over
+ * layers.
+ *
+ * Replaces concat_dicts(list_of_dicts, dim=3), torch.cat over the KV-head
+ * dimension of [B, S, 2, H_j, D] (hexgen/llama/tensor_parallel_dim_concat.py:
+ * 9-19): depth = B, height = 2 S, w_j = H_j * D * elem.
+ */
+int hexkv_head_concat(const hexkv_block *src, int n_layers, int n_shards, void *const *dst_layers,
+                      hexkv_stream_t stream);
+
+/*
  * Cross-process handoff on one GPU.  Two processes sharing the GPU (the
  * prefill and decode ranks of the pilot, hexgen2/run.py:141-198) hand the
  * packed KV buffer over in device memory: the sender exports an IPC handle of

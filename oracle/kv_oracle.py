@@ -19,6 +19,10 @@ Functions and the reference code each one restates:
                                          causal mask :238-241, softmax :242)
                                          evaluated in float64
 * ``packet_payload_bytes``  hexgen2/transport.py:37 (payload accounting)
+* ``flat_concat`` / ``flat_split``  hexgen/llama/kv_cache_communication.py:
+                                         21-26 / 50-57 (flat KV packet)
+* ``batch_pad`` hexgen/llama/kv_cache_batch.py:11-22 (zero-pad + stack)
+* ``concat_dim`` hexgen/llama/tensor_parallel_dim_concat.py:9-19 (TP heads)
 
 Pinning (tests/test_oracle.py): pack/unpack/append against element-by-element
 Python loops on small inputs, the round-trip and untouched-row invariants, and
@@ -26,7 +30,10 @@ the reference's recorded handoff byte counts (evidence/2026-10-19/
 fabric-pilot.json); attend against closed forms (one key -> that value, equal
 keys -> mean of values, a dominant key -> its value, group 1 == MHA), a
 scalar-loop restatement on small shapes, and torch's
-scaled_dot_product_attention in float64.
+scaled_dot_product_attention in float64.  The legacy formats against the
+library routines the reference calls (torch.cat, torch.nn.functional.pad with
+the reference's pad tuple) and against their inverses (slicing a batch or a
+concatenation back into its parts recovers them; padding is zero).
 """
 from __future__ import annotations
 
@@ -157,3 +164,53 @@ def kv_packet_bytes(n_layers: int, prompt_len: int, kv_heads: int, head_dim: int
     [1, L, 2, Hkv, D] live slice per layer (run.py:147-148)."""
     row = 2 * kv_heads * head_dim * elem_bytes
     return 8 + n_layers * prompt_len * row
+
+
+# ---------------------------------------------------------- legacy formats ---
+# The earlier disaggregation scripts (hexgen/llama/) move the KV dict in three
+# more layouts.  All three are element permutations (plus zero padding), so
+# the restatements below work on arrays of any dtype, including integer views
+# of float payloads.
+
+
+def flat_concat(tensors: Sequence[np.ndarray]) -> np.ndarray:
+    """The flat packet of send_key_value_memory_dict: every tensor flattened
+    in row-major order and concatenated (kv_cache_communication.py:21-26)."""
+    parts = [np.asarray(t).reshape(-1) for t in tensors]
+    if not parts:
+        return np.zeros(0)
+    return np.concatenate(parts)
+
+
+def flat_split(flat: np.ndarray, shapes: Sequence[tuple]) -> list:
+    """The receiver's views of the flat packet (kv_cache_communication.py:
+    50-57): consecutive slices reshaped to each shape."""
+    out, off = [], 0
+    for shape in shapes:
+        n = math.prod(shape)
+        out.append(flat[off:off + n].reshape(shape))
+        off += n
+    return out
+
+
+def batch_pad(requests: Sequence[np.ndarray], max_rows: int = None) -> np.ndarray:
+    """One layer of batch_logits_and_key_value_memory_dict (kv_cache_batch.py:
+    11-22): each request's [b_i, S_i, ...] is zero-padded at the end of dim 1
+    to max_rows (default max S_i) and the requests are stacked along dim 0."""
+    if max_rows is None:
+        max_rows = max(r.shape[1] for r in requests)
+    parts = []
+    for r in requests:
+        if r.shape[1] > max_rows:
+            raise ValueError("request longer than max_rows")
+        padded = np.zeros((r.shape[0], max_rows) + r.shape[2:], dtype=r.dtype)
+        padded[:, :r.shape[1]] = r
+        parts.append(padded)
+    return np.concatenate(parts, axis=0)
+
+
+def concat_dim(shards: Sequence[np.ndarray], dim: int = 3) -> np.ndarray:
+    """One key of concat_dicts: the tensor-parallel shards concatenated along
+    `dim`, the KV-head dimension of [B, S, 2, H, D] by default
+    (tensor_parallel_dim_concat.py:9-19)."""
+    return np.concatenate(list(shards), axis=dim)

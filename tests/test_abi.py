@@ -33,19 +33,22 @@ def test_library_exports_every_declared_symbol():
     assert lib.hexkv_last_error() == b""
 
 
-def test_attend_params_layout_matches_c(tmp_path):
-    fields = [f[0] for f in _lib.AttendParams._fields_]
+@pytest.mark.parametrize("c_name,mirror", [("hexkv_attend_params", _lib.AttendParams),
+                                            ("hexkv_block", _lib.Block),
+                                            ("hexkv_ipc_handle", _lib.IpcHandle)])
+def test_struct_layouts_match_c(tmp_path, c_name, mirror):
+    fields = [f[0] for f in mirror._fields_]
     src = tmp_path / "layout.c"
     src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "hexkv.h"\nint main(void){\n'
-                   'printf("%zu\\n", sizeof(hexkv_attend_params));\n'
-                   + "".join(f'printf("%zu\\n", offsetof(hexkv_attend_params, {f}));\n' for f in fields)
+                   f'printf("%zu\\n", sizeof({c_name}));\n'
+                   + "".join(f'printf("%zu\\n", offsetof({c_name}, {f}));\n' for f in fields)
                    + "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)],
                    check=True)
     values = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    assert values[0] == ctypes.sizeof(_lib.AttendParams)
-    assert values[1:] == [getattr(_lib.AttendParams, f).offset for f in fields]
+    assert values[0] == ctypes.sizeof(mirror)
+    assert values[1:] == [getattr(mirror, f).offset for f in fields]
 
 
 def test_header_compiles_as_cxx(tmp_path):
@@ -73,6 +76,31 @@ def test_validation_fails_before_launch():
     assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_ERANGE
     # nothing to do is not an error
     assert lib.hexkv_pack(ptr, ptr, 0, 1, 8, 8, 512, lens, None) == _lib.HEXKV_OK
+
+
+def test_legacy_format_validation_fails_before_launch():
+    lib = _lib.load()
+    B = _lib.Block
+    ptr = (ctypes.c_void_p * 2)(16, 32)
+    # negative size, missing data pointer, missing destination
+    assert lib.hexkv_flat_concat((B * 1)(B(16, -1, 1, 1, 0, 0)), 1, 64, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_flat_concat((B * 1)(B(None, 8, 1, 1, 8, 8)), 1, 64, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_flat_concat((B * 1)(B(16, 8, 1, 1, 8, 8)), 1, None, None) == _lib.HEXKV_EINVAL
+    # empty blocks move nothing
+    assert lib.hexkv_flat_concat((B * 1)(B(None, 8, 0, 1, 8, 8)), 1, None, None) == _lib.HEXKV_OK
+    # a request longer than max_rows; widths or sizes that differ over layers
+    two = (B * 2)(B(16, 512, 5, 1, 512, 2560), B(32, 512, 5, 1, 512, 2560))
+    assert lib.hexkv_batch_pad(two, 2, 1, ptr, 4, None) == _lib.HEXKV_ERANGE
+    assert b"max_rows" in lib.hexkv_last_error()
+    two[1].height = 4
+    assert lib.hexkv_batch_pad(two, 2, 1, ptr, 8, None) == _lib.HEXKV_EINVAL
+    two[1].height, two[1].width = 5, 256
+    assert lib.hexkv_batch_pad(two, 2, 1, ptr, 8, None) == _lib.HEXKV_EINVAL
+    # shards of one layer with different heights; a shard width that changes over layers
+    shards = (B * 2)(B(16, 256, 6, 2, 256, 1536), B(32, 256, 5, 2, 256, 1280))
+    assert lib.hexkv_head_concat(shards, 1, 2, ptr, None) == _lib.HEXKV_EINVAL
+    shards[1].height, shards[1].width = 6, 512
+    assert lib.hexkv_head_concat(shards, 2, 1, ptr, None) == _lib.HEXKV_EINVAL
 
 
 def test_status_codes_map_to_reference_exception_types():

@@ -84,6 +84,28 @@ def test_pack_into_per_layer_views_and_strided_batch(device):
         np.testing.assert_array_equal(bits(out[l]), expect[l])
 
 
+def test_stacked_tensors_match_layer_lists(device):
+    # one [n_layers, B, S, *row] tensor (here a strided view: capacity 9 of 12)
+    # and a stacked [n_layers, T, *row] packed tensor address the same bytes
+    # as the per-layer lists
+    g = torch.Generator(device=device).manual_seed(9)
+    big = torch.randn((3, 4, 12, 2, 2, 16), generator=g, device=device).to(torch.bfloat16)
+    cache = big[:, :, :9]
+    lens = [9, 0, 2, 5]
+    packed = torch.empty((3, 16, 2, 2, 16), dtype=torch.bfloat16, device=device)
+    ops.pack_live(cache, lens, out=packed)
+    expect = oracle.pack([bits(cache[l]) for l in range(3)], lens)
+    np.testing.assert_array_equal(bits(packed), expect)
+    dst = torch.full((3, 4, 9, 2, 2, 16), 7.0, dtype=torch.bfloat16, device=device)
+    sentinel = bits(dst[0])
+    ops.unpack_live(packed, dst, lens)
+    want = oracle.unpack(expect, [sentinel] * 3, lens)
+    for l in range(3):
+        np.testing.assert_array_equal(bits(dst[l]), want[l])
+    with pytest.raises(ValueError, match="contiguous"):
+        ops.pack_live(cache, lens, out=packed[:, :8])
+
+
 def test_unaligned_pointer_uses_narrow_vectors(device):
     base = torch.randn(2 * 9 * 16 + 2, device=device).to(torch.float16)
     cache = base[2:].view(2, 9, 2, 1, 8)  # 4-byte aligned, not 16-byte aligned

@@ -176,3 +176,91 @@ def test_attend_scale_default_is_inverse_sqrt_head_dim():
     q, cache = _rand_attn(rng, 1, 1, 2, 2, 16, 5)
     np.testing.assert_allclose(oracle.attend(q, cache, [5]),
                                oracle.attend(q, cache, [5], softmax_scale=1 / math.sqrt(16)), atol=0)
+
+
+# ---------------------------------------------------------- legacy formats ---
+# Pinned against the library routines the reference calls (torch.cat,
+# torch.nn.functional.pad with the reference's own pad tuple) and against the
+# inverses (slicing the result back into its parts).
+
+def _rand(rng, shape):
+    return rng.standard_normal(shape).astype(np.float32)
+
+
+def test_flat_concat_is_torch_cat_of_flattened_and_splits_back():
+    rng = np.random.default_rng(1)
+    base = _rand(rng, (2, 6, 2, 3, 4))
+    tensors = [base[:, :5], _rand(rng, (1, 3, 2, 3, 4)), base.transpose(1, 0, 2, 3, 4), _rand(rng, (0, 4))]
+    flat = oracle.flat_concat(tensors)
+    want = torch.cat([torch.from_numpy(np.ascontiguousarray(t)).flatten() for t in tensors]).numpy()
+    np.testing.assert_array_equal(flat, want)
+    for got, t in zip(oracle.flat_split(flat, [t.shape for t in tensors]), tensors):
+        np.testing.assert_array_equal(got, t)
+
+
+def test_flat_packet_of_reference_example_shapes():
+    # kv_cache_communication.py:75-84: 32 layers of [1, 150, 2, 32, 128]
+    shapes = [(1, 150, 2, 32, 128)] * 32
+    assert sum(math.prod(s) for s in shapes) == 32 * 150 * 2 * 32 * 128
+    flat = oracle.flat_concat([np.full(s[1:2], i, dtype=np.int16) for i, s in enumerate(shapes)])
+    assert flat.shape == (32 * 150,) and flat[150 * 7] == 7
+
+
+def test_batch_pad_is_reference_pad_then_cat():
+    rng = np.random.default_rng(2)
+    reqs = [_rand(rng, (1, 5, 2, 3, 4)), _rand(rng, (3, 2, 2, 3, 4)), _rand(rng, (2, 0, 2, 3, 4)),
+            _rand(rng, (1, 7, 2, 3, 4))]
+    got = oracle.batch_pad(reqs)
+    # kv_cache_batch.py:17-22 verbatim semantics: F.pad(t, (0,0,0,0,0,0,0,pad)) then cat(dim=0)
+    import torch.nn.functional as F
+    parts = []
+    for r in reqs:
+        t = torch.from_numpy(r)
+        pad = 7 - t.size(1)
+        parts.append(F.pad(t, (0, 0, 0, 0, 0, 0, 0, pad), "constant", 0) if pad > 0 else t)
+    np.testing.assert_array_equal(got, torch.cat(parts, dim=0).numpy())
+    # inverse: each request comes back from its rows; the padding is zero
+    row = 0
+    for r in reqs:
+        b, s = r.shape[:2]
+        np.testing.assert_array_equal(got[row:row + b, :s], r)
+        assert not got[row:row + b, s:].any()
+        row += b
+    assert got.shape == (7, 7, 2, 3, 4)
+
+
+def test_batch_pad_reference_example_shapes():
+    # kv_cache_batch.py:38-44: [1, 150, ...] and [1, 128, ...] -> [2, 150, ...]
+    a, b = np.ones((1, 150, 2, 1, 2), np.float32), np.ones((1, 128, 2, 1, 2), np.float32)
+    got = oracle.batch_pad([a, b])
+    assert got.shape == (2, 150, 2, 1, 2)
+    assert got[1, 127].all() and not got[1, 128:].any() and got[0].all()
+    with pytest.raises(ValueError):
+        oracle.batch_pad([a], max_rows=100)
+
+
+@pytest.mark.parametrize("dim", [3, -2, 0, 1, 4])
+def test_concat_dim_is_torch_cat_and_splits_back(dim):
+    rng = np.random.default_rng(3)
+    heads = [1, 3, 2]
+    shards = []
+    for h in heads:
+        shape = [2, 4, 2, 2, 5]
+        shape[dim % 5] = h
+        shards.append(_rand(rng, tuple(shape)))
+    got = oracle.concat_dim(shards, dim)
+    np.testing.assert_array_equal(got, torch.cat([torch.from_numpy(s) for s in shards], dim=dim).numpy())
+    pieces = np.split(got, np.cumsum(heads)[:-1], axis=dim)
+    for p, s in zip(pieces, shards):
+        np.testing.assert_array_equal(p, s)
+
+
+def test_concat_dim_default_is_the_kv_head_dim():
+    # tensor_parallel_dim_concat.py:9: dim=3 of [B, S, 2, H, D] joins the heads,
+    # so kv head h of the result is shard h // Hs's head h % Hs
+    rng = np.random.default_rng(4)
+    shards = [_rand(rng, (2, 3, 2, 2, 4)) for _ in range(4)]
+    got = oracle.concat_dim(shards)
+    assert got.shape == (2, 3, 2, 8, 4)
+    for h in range(8):
+        np.testing.assert_array_equal(got[:, :, :, h], shards[h // 2][:, :, :, h % 2])

@@ -22,14 +22,14 @@
 //   are v_dot2_f32_{bf16,f16} (fp32: fma) of the lane's K slice with its
 //   slice of the G query vectors, summed over the LPP lanes by DPP moves.
 //
-// attend_mfma_kernel (16-bit, the GQA group on a matrix core): a wave takes
-//   tiles of 16 positions.  K is loaded in the A-operand layout of
-//   v_mfma_f32_16x16x32_{bf16,f16} (lane = position, 16-byte head slices) and
-//   the G query heads of the group are the B operand, so D/32 MFMAs give the
-//   16 x G score tile with no cross-lane reduction.  The probabilities go
-//   through a small per-wave LDS tile to the lanes that hold V (one position
-//   per LPP lanes, as above).  The matrix core works on 16 columns of which G
-//   are used; it is idle otherwise, and the VALU work per byte drops.
+// attend_mfma_kernel (16-bit, head_dim >= 64): both products on the matrix
+//   cores.  A wave takes tiles of 16 positions; S = K Q^T is
+//   v_mfma_f32_16x16x32 with K in the A-operand layout (lane = position,
+//   16-byte head slices) and the G query heads as the B operand, and the
+//   resulting score layout is directly the A operand of O += P V
+//   (v_mfma_f32_16x16x16, probabilities as hi + lo 16-bit pairs).  V passes
+//   through a per-wave LDS tile and comes back transposed
+//   (ds_read_b64_tr_b16) as the B operand.  The VALU only runs the softmax.
 //
 // With kv_new (fused append) the new row is the last position of the row: it
 // is never read from the cache; one wave attends it from kv_new after the
@@ -429,43 +429,90 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
 
 // ------------------------------------------------------------- MFMA path ---
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// LDS view of a byte offset into a __shared__ array.
+__device__ __forceinline__ lds_s16x4 *lds_at(char *shared, uint32_t off) {
+  return (lds_s16x4 *)((__attribute__((address_space(3))) char *)shared + off);
+}
+
 template <typename T>
 struct Mfma;
 
 template <>
 struct Mfma<__bf16> {
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  // 16x16x32: scores, K slices (A) against the group's query heads (B)
   __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
+  }
+  // 16x16x16: probabilities (A) against transposed V (B)
+  __device__ __forceinline__ static f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  // f rounded to bf16: (bits, value as float)
+  __device__ __forceinline__ static short round(float f, float *r) {
+    const short b = __builtin_bit_cast(short, static_cast<__bf16>(f));
+    *r = __uint_as_float(static_cast<unsigned int>(static_cast<unsigned short>(b)) << 16);
+    return b;
   }
 };
 
 template <>
 struct Mfma<_Float16> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v4 __attribute__((ext_vector_type(4)));
   __device__ __forceinline__ static f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), c, 0, 0, 0);
   }
+  __device__ __forceinline__ static f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4, a), __builtin_bit_cast(v4, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static short round(float f, float *r) {
+    const _Float16 h = static_cast<_Float16>(f);
+    *r = static_cast<float>(h);
+    return __builtin_bit_cast(short, h);
+  }
 };
 
-// Lane layouts of one wave and a 16-position tile:
-//   scores  lane l = (kg = l / 16, r = l % 16).  As the MFMA A operand lane l
-//           holds position r's 16-byte K slices 4j + kg (j < D/32, one per
-//           k-step); as the B operand it holds the same slices of query head
-//           r (zero for r >= G).  The result gives lane l the scores of
-//           positions 4 kg + e (e < 4) for head r.
-//   values  lane l = (vg = l / VLPP, vs = l % VLPP): position u VPPI + vg
-//           (u < UV), 16-byte slice vs, 8 elements per lane.
+// Both products of a 16-position tile on the matrix cores.
+//
+//   scores  S = K Q^T with v_mfma_f32_16x16x32: lane l = (kg = l / 16,
+//           r = l % 16) holds, as the A operand, position r's 16-byte K
+//           slices 4j + kg (j < D/32) and, as the B operand, the same slices
+//           of query head r (zero for r >= G).  The result gives lane l the
+//           scores of positions 4 kg + e (e < 4) for head r.
+//   values  O += P V with v_mfma_f32_16x16x16 per 16 columns of V: that
+//           score layout is already the A operand (lane (kg, r): head r,
+//           positions 4 kg + e), so the probabilities stay in registers.  V
+//           is staged row-major in a per-wave LDS tile and read back
+//           transposed by ds_read_b64_tr_b16, which hands lane 4c + d of each
+//           16-lane group element d of the 8 bytes addressed by lanes c,
+//           c + 4, c + 8, c + 12: with lane s of group kg addressing V row
+//           4 kg + s / 4, columns n0 + 4 (s % 4).., lane (kg, n) receives
+//           V[4 kg + e][n0 + n], e < 4 -- the B operand.  The accumulator lane
+//           (kg, n) holds O[head 4 kg + e][n0 + n].
+//
+// The probabilities enter the product as hi + lo pairs of the input type, so
+// the products carry about 17 bits of each probability; scores, sums and O
+// stay in fp32.
+//
+// Three waves per SIMD (at most 168 registers per lane): measured faster than
+// two (more registers, accumulators in AGPRs) and than four on the
+// Llama-2-70B TP-8 share (16.8 vs 19.7 and 18.4 us per layer).
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendArgs a) {
+__global__ __launch_bounds__(kAttThreads, 3) void attend_mfma_kernel(const AttendArgs a) {
   static_assert(sizeof(T) == 2 && G <= 16, "MFMA path: 16-bit types, up to 16 heads per group");
-  using E = Elem<T>;
-  constexpr int NJ = D / 32;       // k-steps of 32 elements
-  constexpr int VLPP = D / 8;      // value lanes per position
-  constexpr int VPPI = 64 / VLPP;  // positions per value load
-  constexpr int UV = 16 / VPPI;    // value loads per tile
+  using M = Mfma<T>;
+  constexpr int NJ = D / 32;         // score k-steps of 32 elements
+  constexpr int NC = D / 16;         // value column chunks of 16
+  constexpr int VLPP = D / 8;        // lanes per V row (16 bytes each)
+  constexpr int VPPI = 64 / VLPP;    // V rows per load
+  constexpr int UV = 16 / VPPI;      // V loads per tile
+  constexpr int PITCH = 2 * D + 32;  // LDS bytes per staged V row (padded: transposed reads spread over banks)
   static_assert(NJ >= 1 && VLPP <= 64 && UV >= 1 && UV * VPPI == 16, "head_dim");
-  __shared__ float s_p[kAttWaves][16][G];
+  __shared__ __attribute__((aligned(16))) char s_v[kAttWaves][16 * PITCH];
   __shared__ float s_acc[kAttWaves][G][D];
   __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
   Work w;
@@ -490,19 +537,22 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
   const uint32_t k_lane = static_cast<uint32_t>(w.p0 + r) * row_bytes + kg * 16;
   const uint32_t v_lane = static_cast<uint32_t>(w.p0 + vg) * row_bytes + vs * 16;
 
-  // Score-layout state (lane r holds head r; m uniform over the 4 kg lanes).
-  float m = kNoScore, lp = 0.f;
-  // Value-layout accumulators.
-  float acc[G][8];
+  // This wave's V tile: row-major stores, transposed reads.
+  char *vtile = s_v[wave];
+  const uint32_t v_store = vg * PITCH + vs * 16;
+  const uint32_t v_read = (4 * kg + r / 4) * PITCH + (r % 4) * 8;
+
+  float m = kNoScore, lp = 0.f;  // head r's running max and this lane's share of its sum
+  f32x4 acc[NC];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // One tile of 16 positions starting at p0 + i0: `fetch` issues its loads
   // (MODE 0 full, 1 tail: positions past n_cache clamped to the last cached
-  // one, 2: the new row from kv_new, written to the cache by the writer);
-  // `consume` computes it (masking what MODE 1 and 2 do not attend).
+  // one, 2: the new row from kv_new in every slot, written to the cache by
+  // the writer); `consume` computes it (masking what MODE 1 and 2 do not
+  // attend).  Every staged V row holds finite data, so masked (zero)
+  // probabilities contribute exact zeros.
   auto fetch = [&](int i0, u32x4 (&kr)[NJ], u32x4 (&vr)[UV], auto mode) {
     constexpr int MODE = decltype(mode)::value;
     if constexpr (MODE == 2) {
@@ -539,9 +589,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
   };
   auto consume = [&](int i0, const u32x4 (&kr)[NJ], const u32x4 (&vr)[UV], auto mode) {
     constexpr int MODE = decltype(mode)::value;
+    // Stage V while the scores are computed.
+#pragma unroll
+    for (int u = 0; u < UV; ++u) *reinterpret_cast<u32x4 *>(vtile + v_store + u * VPPI * PITCH) = vr[u];
     f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) c = Mfma<T>::mma(kr[j], qb[j], c);
+    for (int j = 0; j < NJ; ++j) c = M::mma(kr[j], qb[j], c);
     float s[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -549,44 +602,41 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
       if constexpr (MODE == 1) s[e] = i0 + 4 * kg + e < w.n_cache ? s[e] : -INFINITY;
       if constexpr (MODE == 2) s[e] = (kg == 0 && e == 0) ? s[e] : -INFINITY;
     }
-    float mt = max_from<16>(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))) * scale;
+    const float mt = max_from<16>(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))) * scale;
     const bool up = head_lane && mt > m + kRescaleSlack;
     if (__any(up)) {
       const float mnew = up ? mt : m;
       const float cf = fast_exp2(m - mnew);
       m = mnew;
       lp *= cf;
+      // accumulator rows are heads 4 kg + e; lane h (< 16) holds head h's factor
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float cg = readlane_f(cf, g);
+      for (int e = 0; e < 4; ++e) {
+        const float ce = __shfl(cf, 4 * kg + e);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] *= cg;
+        for (int ch = 0; ch < NC; ++ch) acc[ch][e] *= ce;
       }
     }
-    float p[4];
+    // Each probability enters the product as the sum of two 16-bit values
+    // (p = hi + lo to about 2^-17 relative); both products with the 16-bit V
+    // are exact in the fp32 accumulator, and the sum takes hi + lo too.
+    s16x4 pa_hi, pa_lo;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      p[e] = fast_exp2(fmaf(s[e], scale, -m));
-      lp += p[e];
-    }
-    if (head_lane) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s_p[wave][4 * kg + e][r] = p[e];
+      const float p = head_lane ? fast_exp2(fmaf(s[e], scale, -m)) : 0.f;
+      float hi, lo;
+      pa_hi[e] = M::round(p, &hi);
+      pa_lo[e] = M::round(p - hi, &lo);
+      lp += hi + lo;
     }
     __builtin_amdgcn_wave_barrier();
+    // (V is read twice from LDS rather than held: fewer registers.)
 #pragma unroll
-    for (int u = 0; u < UV; ++u) {
-      const float *pp = s_p[wave][u * VPPI + vg];
-      float pg[G];
+    for (int ch = 0; ch < NC; ++ch)
+      acc[ch] = M::mma16(pa_hi, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_at(vtile, v_read + ch * 32)), acc[ch]);
 #pragma unroll
-      for (int g = 0; g < G; ++g) pg[g] = pp[g];
-      float vf[8];
-      E::to_float(vr[u], vf);
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], vf[e], acc[g][e]);
-    }
+    for (int ch = 0; ch < NC; ++ch)
+      acc[ch] = M::mma16(pa_lo, __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_at(vtile, v_read + ch * 32)), acc[ch]);
     __builtin_amdgcn_wave_barrier();
   };
 
@@ -621,18 +671,16 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
     consume(0, kr, vr, std::integral_constant<int, 2>{});
   }
 
-  // Wave totals: l over the 4 kg lanes of each head, o over the value lanes
-  // of each slice.
+  // Wave totals: l over the 4 kg lanes of each head; O rows from the
+  // accumulator layout.
   lp = sum_from<16>(lp);
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int e = 0; e < 4; ++e) {
+    const int h = 4 * kg + e;
+    if (h < G) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = sum_from<VLPP>(acc[g][e]);
-  if (lane < VLPP) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wave][g][vs * 8 + e] = acc[g][e];
+      for (int ch = 0; ch < NC; ++ch) s_acc[wave][h][ch * 16 + r] = acc[ch][e];
+    }
   }
   if (lane < G) {
     s_m[wave][lane] = m;
@@ -644,12 +692,18 @@ __global__ __launch_bounds__(kAttThreads) void attend_mfma_kernel(const AttendAr
 
 // Merges the partitions of one (query row, query head) of a split row:
 // o = sum_p w_p o_p with w_p = 2^(m_p - max m) / sum_p 2^(m_p - max m) l_p.
-// One wave reduces (max, sum) over the partitions and stages the weights in
-// LDS; the 256 threads then split the partitions into 256 / D slices of D
-// outputs each (all loads of a slice issued 8 at a time) and add the slices
-// through LDS.  One workgroup per (head, row) keeps the per-workgroup chain
-// short when a few long rows carry many partitions.
+// One workgroup per (head, row) keeps the per-workgroup chain short when a
+// few long rows carry many partitions.  The 256 threads split the partitions
+// into 256 / D slices of D outputs each and add the slices through LDS.
+//
+// Fast path (up to kCombineDepth partitions per slice, the decode shapes):
+// every load -- the row length, each partition's (max, sum) and this
+// thread's partial outputs -- is issued up front for the host bound
+// max_parts and masked afterwards by the row's own partition count, so the
+// workgroup waits for one round of memory latency instead of three.
+// Otherwise the weights are staged in LDS kCombineChunk partitions at a time.
 constexpr int kCombineChunk = 256;  // partitions whose weights sit in LDS at once
+constexpr int kCombineDepth = 32;   // partial outputs per thread held in registers
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a) {
@@ -658,17 +712,75 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
   constexpr int PER = (D + kAttThreads - 1) / kAttThreads;        // outputs per thread (D > 256)
   __shared__ float s_w[kCombineChunk];
   __shared__ float s_red[SL][D];
+  __shared__ float s_wmax[kAttWaves], s_wsum[kAttWaves];
   __shared__ float s_mx, s_inv;
   const int h = blockIdx.x, row = blockIdx.y;
   const int b = row / a.q_len, t = row - b * a.q_len;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int64_t base = (static_cast<int64_t>(row) * a.q_heads + h) * a.max_parts;
+  const float *ml = a.ws_ml + base * 2;
+  const int d0 = tid % D, sl = tid / D;
+  T *out = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + static_cast<int64_t>(h) * D;
+
+  if constexpr (PER == 1) {
+    if (a.max_parts <= kCombineChunk && a.max_parts <= SL * kCombineDepth) {
+      float2 mlv = {-INFINITY, 0.f};
+      if (tid < a.max_parts) mlv = *reinterpret_cast<const float2 *>(ml + 2 * tid);
+      float ov[kCombineDepth];
+      const float *o = a.ws_o + base * D + d0;
+#pragma unroll
+      for (int k = 0; k < kCombineDepth; ++k) {
+        const int p = sl + k * SL;
+        ov[k] = 0.f;
+        if (sl < SL && p < a.max_parts) ov[k] = o[static_cast<int64_t>(p) * D];
+      }
+      int pos_new;
+      const int len = row_length(a, b, t, &pos_new);
+      const int nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
+      if (nparts <= 1) return;  // written by the attention kernel
+      const bool valid = tid < nparts;
+      const float mp = valid ? mlv.x : -INFINITY;
+      float mx = wave_max(mp);
+      if ((tid & 63) == 0) s_wmax[wave] = mx;
+      __syncthreads();
+      mx = s_wmax[0];
+#pragma unroll
+      for (int w = 1; w < kAttWaves; ++w) mx = fmaxf(mx, s_wmax[w]);
+      const float c = valid ? fast_exp2(mp - mx) : 0.f;
+      s_w[tid] = c;
+      const float sum = sum_from<1>(valid ? c * mlv.y : 0.f);
+      if ((tid & 63) == 0) s_wsum[wave] = sum;
+      __syncthreads();
+      float total = 0.f;
+#pragma unroll
+      for (int w = 0; w < kAttWaves; ++w) total += s_wsum[w];
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < kCombineDepth; ++k) {
+        const int p = sl + k * SL;
+        if (sl < SL && p < nparts) acc = fmaf(s_w[p], ov[k], acc);
+      }
+      if constexpr (SL > 1) {
+        if (sl < SL) s_red[sl][d0] = acc;
+        __syncthreads();
+        if (tid < D) {
+          float r = 0.f;
+#pragma unroll
+          for (int k = 0; k < SL; ++k) r += s_red[k][tid];
+          out[tid] = E::from_float(r / total);
+        }
+      } else {
+        if (sl == 0) out[d0] = E::from_float(acc / total);
+      }
+      return;
+    }
+  }
+
   int pos_new;
   const int len = row_length(a, b, t, &pos_new);
   if (len <= 0) return;
   const int nparts = (len + a.part - 1) / a.part;
   if (nparts <= 1) return;
-  const int tid = threadIdx.x;
-  const int64_t base = (static_cast<int64_t>(row) * a.q_heads + h) * a.max_parts;
-  const float *ml = a.ws_ml + base * 2;
   if (tid < 64) {
     float mx = kNoScore;
     for (int p = tid; p < nparts; p += 64) mx = fmaxf(mx, ml[2 * p]);
@@ -681,7 +793,6 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
       s_inv = 1.f / sum;
     }
   }
-  const int d0 = tid % D, sl = tid / D;
   float acc[PER];
 #pragma unroll
   for (int k = 0; k < PER; ++k) acc[k] = 0.f;
@@ -706,7 +817,6 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
       }
     }
   }
-  T *out = static_cast<T *>(a.out) + b * a.o_bs + t * a.o_rs + static_cast<int64_t>(h) * D;
   if constexpr (SL > 1) {
     if (sl < SL) s_red[sl][d0] = acc[0];
     __syncthreads();
@@ -822,10 +932,10 @@ constexpr int slots() {
 }
 
 // Kernel choice: the MFMA kernel for 16-bit data with head_dim >= 64 and 8+
-// query heads per KV head, where the matrix core takes enough of the group's
-// dot products to beat the VALU kernel (Llama-2-70B TP-8 share: 28.5 vs
-// 30.6 us; TinyLlama: 10.2 vs 10.8 us); the VALU kernel otherwise (Llama-3-8B,
-// group 4: 172.6 vs 181.7 us).
+// query heads per KV head, where it beats the VALU kernel (Llama-2-70B TP-8
+// share: 16.0 vs 23.8 us per layer at the best partition of each; TinyLlama:
+// 10.6 vs 11.9); the VALU kernel otherwise (Llama-3-8B, group 4: 176.4 vs
+// 180.6; Llama-2-7B, group 1: 34.8 vs 38.1).
 static bool use_mfma(const hexkv_attend_params *p, int G) {
   if (p->kernel == HEXKV_KERNEL_MFMA) return true;
   if (p->kernel == HEXKV_KERNEL_VALU) return false;

@@ -37,6 +37,8 @@ struct RaggedCopyArgs {
   int32_t cu[HEXKV_MAX_SEQS_PER_LAUNCH + 1];  // packed row offset of each sequence
 };
 
+// Every pass issues kCopyUnroll loads per lane before its stores; the last,
+// partial pass masks lanes instead of falling back to one vector at a time.
 template <typename V>
 __device__ __forceinline__ void copy_span(const char *__restrict__ s, char *__restrict__ d,
                                           int64_t n) {
@@ -51,7 +53,15 @@ __device__ __forceinline__ void copy_span(const char *__restrict__ s, char *__re
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) __builtin_nontemporal_store(r[u], dv + i + u * kCopyThreads);
   }
-  for (; i < nv; i += kCopyThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(sv + i), dv + i);
+  if (i < nv) {
+    V r[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u)
+      if (i + u * kCopyThreads < nv) r[u] = __builtin_nontemporal_load(sv + i + u * kCopyThreads);
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u)
+      if (i + u * kCopyThreads < nv) __builtin_nontemporal_store(r[u], dv + i + u * kCopyThreads);
+  }
 }
 
 // PACK: src = padded cache, dst = packed buffer.  UNPACK: the reverse.

@@ -111,7 +111,9 @@ class Job:
         1. calibration: the pack kernel on one contiguous 2 GiB sequence, which
            is a plain copy of exactly 2 GiB read + 2 GiB written;
         2. pack of the workload; 3. unpack of the workload;
-        4. decode step 0 over every layer (fused append + attend).
+        4. decode step 0 over every layer (fused append + attend);
+        then (formats_traffic_probe, after the job's buffers are freed) one
+        call of each legacy format.
         """
         w = self.w
         rows = (2 << 30) // w.row_bytes
@@ -130,6 +132,16 @@ class Job:
         torch.cuda.synchronize()
         log("probe done")
 
+    @staticmethod
+    def formats_traffic_probe(device):
+        """5. one call of each legacy format, in format_cases order."""
+        cases = format_cases(device)
+        torch.cuda.synchronize()
+        for name, run, nbytes, launches, _ in cases:
+            log(f"format {name}: {launches} launches, {nbytes} algorithmic bytes")
+            run()
+        torch.cuda.synchronize()
+
     def verify(self):
         """Size-independent self-check on the full workload: the unpacked live
         rows equal the prefill cache's (before any append) and the packed
@@ -145,16 +157,16 @@ class Job:
             start += n
 
 
-def measure_formats(device, reps=5):
-    """Secondary figures, outside the timed steps: the legacy KV formats
-    (hexgen2_amd.kv_formats) on Llama-shaped synthetic data, each GB/s of
-    algorithmic bytes (bytes read + bytes written, zero padding included):
+def format_cases(device):
+    """The legacy KV formats (hexgen2_amd.kv_formats) on Llama-shaped
+    synthetic data, as (name, run, algorithmic bytes, launches, extra):
+    algorithmic bytes = bytes read + bytes written, zero padding included.
 
-    * flat packet: 32 layers of one request's live [1, 8192, 2, 8, 128] bf16
+    * flat_packet: 32 layers of one request's live [1, 8192, 2, 8, 128] bf16
       slice of an 8448-position cache, flattened and concatenated;
-    * zero-pad batching: 8 requests of lengths U[128, 4096] (seed 0), 32
-      layers of [1, L_i, 2, 8, 128] bf16, padded to the longest and stacked;
-    * TP head concat: 16 layers of 8 tensor-parallel shards [8, 4096, 2, 1,
+    * zero_pad_batch: 8 requests of lengths U[128, 4096] (seed 0), 32 layers
+      of [1, L_i, 2, 8, 128] bf16, padded to the longest and stacked;
+    * tp_head_concat: 16 layers of 8 tensor-parallel shards [8, 4096, 2, 1,
       128] bf16 (Llama-2-70B's KV heads over TP 8) joined into one
       [8, 4096, 2, 8, 128] cache per layer.
     """
@@ -162,42 +174,44 @@ def measure_formats(device, reps=5):
 
     g = torch.Generator(device=device).manual_seed(3)
     row = 2 * 8 * 128 * 2
+    spans_per_launch = 32  # kMaxSpans of the span-copy kernel
+    cases = []
+    cache = torch.empty((32, 1, 8448, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
+    layers = [cache[l, :, :8192] for l in range(32)]
+    flat = torch.empty(32 * 8192 * row // 2, dtype=torch.bfloat16, device=device)
+    cases.append(("flat_packet", lambda: kvf.flat_concat(layers, out=flat), 2 * 32 * 8192 * row, 1, {}))
 
-    def timed(fn):
-        fn()
+    lens = [int(x) for x in torch.randint(128, 4097, (8,), generator=torch.Generator().manual_seed(0))]
+    bcache = torch.empty((32, 8, 4096, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
+    dicts = [{l: bcache[l, i:i + 1, :n] for l in range(32)} for i, n in enumerate(lens)]
+    spans = 32 * sum(1 + (n < max(lens)) for n in lens)
+    cases.append(("zero_pad_batch", lambda: kvf.batch_key_value_memory_dicts(dicts),
+                  32 * row * (sum(lens) + 8 * max(lens)), -(-spans // spans_per_launch), {"lens": lens}))
+
+    shards_t = torch.empty((8, 16, 8, 4096, 2, 1, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
+    shards = [{l: shards_t[j, l] for l in range(16)} for j in range(8)]
+    cases.append(("tp_head_concat", lambda: kvf.concat_dicts(shards), 2 * shards_t.numel() * 2,
+                  -(-16 * 8 // spans_per_launch), {}))
+    return cases
+
+
+def measure_formats(device, reps=5):
+    """Secondary figures, outside the timed steps: GB/s of algorithmic bytes
+    of each legacy format (``format_cases``), HIP events over ``reps`` calls."""
+    out = {}
+    for name, run, nbytes, launches, extra in format_cases(device):
+        run()
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         ev[0].record()
         for _ in range(reps):
-            fn()
+            run()
         ev[1].record()
         torch.cuda.synchronize()
-        return ev[0].elapsed_time(ev[1]) / reps
-
-    def entry(nbytes, ms):
+        ms = ev[0].elapsed_time(ev[1]) / reps
         gbs = nbytes / (ms * 1e-3) / 1e9
-        return {"gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "ms": round(ms, 4),
-                "bytes": int(nbytes)}
-
-    out = {}
-    cache = torch.empty((32, 1, 8448, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
-    layers = [cache[l, :, :8192] for l in range(32)]
-    flat = torch.empty(32 * 8192 * row // 2, dtype=torch.bfloat16, device=device)
-    out["flat_packet"] = entry(2 * 32 * 8192 * row, timed(lambda: kvf.flat_concat(layers, out=flat)))
-    del cache, layers, flat
-
-    lens = [int(x) for x in torch.randint(128, 4097, (8,), generator=torch.Generator().manual_seed(0))]
-    cache = torch.empty((32, 8, 4096, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
-    dicts = [{l: cache[l, i:i + 1, :n] for l in range(32)} for i, n in enumerate(lens)]
-    nbytes = 32 * row * (sum(lens) + 8 * max(lens))
-    out["zero_pad_batch"] = entry(nbytes, timed(lambda: kvf.batch_key_value_memory_dicts(dicts)))
-    out["zero_pad_batch"]["lens"] = lens
-    del cache, dicts
-
-    shards_t = torch.empty((8, 16, 8, 4096, 2, 1, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
-    shards = [{l: shards_t[j, l] for l in range(16)} for j in range(8)]
-    out["tp_head_concat"] = entry(2 * shards_t.numel() * 2, timed(lambda: kvf.concat_dicts(shards)))
-    del shards_t, shards
+        out[name] = {"gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "ms": round(ms, 4),
+                     "bytes": int(nbytes), "launches": launches, **extra}
     torch.cuda.empty_cache()
     return out
 
@@ -261,6 +275,9 @@ def main():
     log("buffers ready")
     if args.traffic_probe:
         job.traffic_probe()
+        del job
+        torch.cuda.empty_cache()
+        Job.formats_traffic_probe(device)
         return
     if not args.no_verify:
         job.verify()

@@ -697,15 +697,17 @@ __global__ __launch_bounds__(kAttThreads, 3) void attend_mfma_kernel(const Atten
 // into 256 / D slices of D outputs each and add the slices through LDS.
 //
 // Fast path (up to kCombineDepth partitions per slice, the decode shapes):
-// every load -- the row length, each partition's (max, sum) and this
-// thread's partial outputs -- is issued up front for the host bound
-// max_parts and masked afterwards by the row's own partition count, so the
-// workgroup waits for one round of memory latency instead of three.
+// once the row length is in, every partition's (max, sum) and this thread's
+// partial outputs are loaded at once, so the workgroup waits for two rounds
+// of memory latency instead of three (length, then (max, sum), then the
+// outputs behind a barrier) and reads only the row's own partitions.
 // Otherwise the weights are staged in LDS kCombineChunk partitions at a time.
 constexpr int kCombineChunk = 256;  // partitions whose weights sit in LDS at once
-constexpr int kCombineDepth = 32;   // partial outputs per thread held in registers
 
-template <typename T, int D, int G>
+// kCombineDepth: partial outputs per thread held in registers, 8 or 32,
+// chosen by the host from max_parts (the smaller instance keeps every
+// workgroup of a large decode batch resident at once).
+template <typename T, int D, int G, int kCombineDepth>
 __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a) {
   using E = Elem<T>;
   constexpr int SL = kAttThreads / D >= 1 ? kAttThreads / D : 1;  // partition slices
@@ -724,21 +726,21 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
 
   if constexpr (PER == 1) {
     if (a.max_parts <= kCombineChunk && a.max_parts <= SL * kCombineDepth) {
+      int pos_new;
+      const int len = row_length(a, b, t, &pos_new);
+      const int nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
+      if (nparts <= 1) return;  // written by the attention kernel
+      const bool valid = tid < nparts;
       float2 mlv = {-INFINITY, 0.f};
-      if (tid < a.max_parts) mlv = *reinterpret_cast<const float2 *>(ml + 2 * tid);
+      if (valid) mlv = *reinterpret_cast<const float2 *>(ml + 2 * tid);
       float ov[kCombineDepth];
       const float *o = a.ws_o + base * D + d0;
 #pragma unroll
       for (int k = 0; k < kCombineDepth; ++k) {
         const int p = sl + k * SL;
         ov[k] = 0.f;
-        if (sl < SL && p < a.max_parts) ov[k] = o[static_cast<int64_t>(p) * D];
+        if (sl < SL && p < nparts) ov[k] = o[static_cast<int64_t>(p) * D];
       }
-      int pos_new;
-      const int len = row_length(a, b, t, &pos_new);
-      const int nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
-      if (nparts <= 1) return;  // written by the attention kernel
-      const bool valid = tid < nparts;
       const float mp = valid ? mlv.x : -INFINITY;
       float mx = wave_max(mp);
       if ((tid & 63) == 0) s_wmax[wave] = mx;
@@ -950,7 +952,12 @@ static void launch(const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
   } else {
     attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
   }
-  if (a.max_parts > 1) combine_kernel<T, D, G><<<dim3(a.q_heads, grid.z), kAttThreads, 0, s>>>(a);
+  if (a.max_parts > 1) {
+    const dim3 cgrid(a.q_heads, grid.z);
+    constexpr int SL = kAttThreads / D >= 1 ? kAttThreads / D : 1;
+    if (a.max_parts <= 8 * SL) combine_kernel<T, D, G, 8><<<cgrid, kAttThreads, 0, s>>>(a);
+    else combine_kernel<T, D, G, 32><<<cgrid, kAttThreads, 0, s>>>(a);
+  }
 }
 
 template <typename T, int D>

@@ -19,11 +19,14 @@
 
 namespace hexkv {
 
-// 256 threads x 4 vectors of 16 bytes in flight per workgroup.  A chunked
-// copy of this shape moves 5.55 TB/s (read + write) on MI355X, a
-// device-to-device hipMemcpy 4.90; 512 threads measured 2% faster on one
-// contiguous 8 GiB copy but 2.5% slower on the ragged pack/unpack.
-constexpr int kCopyThreads = 256;
+// 512 threads x 4 vectors of 16 bytes in flight per workgroup, chunks of at
+// most 128 KB.  Measured on MI355X with the Llama-3-8B handoff (pack + unpack
+// of 2 x 63.9 GB): 23.24-23.32 ms against 23.48-23.50 for 256 threads and
+// 256 KB chunks, 24.1 for 512 threads and 256 KB, 23.8 for 1024 x 2.  For
+// reference a plain chunked copy reaches 5.55-5.76 TB/s (read + write), a
+// device-to-device hipMemcpy 4.90, a write-only stream 6.2-6.4 and a
+// read-only stream 7.1.
+constexpr int kCopyThreads = 512;
 constexpr int kCopyUnroll = 4;
 
 struct RaggedCopyArgs {
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(kCopyThreads) void append_kernel(
 static int64_t choose_chunk(int64_t total_bytes) {
   const int64_t target_wgs = 8192;
   int64_t chunk = (total_bytes / target_wgs + 4095) / 4096 * 4096;
-  return std::min<int64_t>(std::max<int64_t>(chunk, 16384), 262144);
+  return std::min<int64_t>(std::max<int64_t>(chunk, 16384), 131072);
 }
 
 static int ragged_copy(bool pack, const void *const *src_layers, void *const *dst_layers,

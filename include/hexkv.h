@@ -2,13 +2,15 @@
  * hexkv.h -- C ABI of the MI355X (gfx950) KV-cache data path of HexGen-2's
  * disaggregated prefill/decode pilot.
  *
- * Three steps, each a hand-written HIP kernel:
+ * The steps, each a hand-written HIP kernel:
  *   pack    gather the live positions of every layer's prefill cache into one
  *           contiguous handoff buffer (ragged, prefix-sum offsets, no padding);
  *   unpack  scatter that buffer into the decode phase's preallocated cache;
  *   append  write the new token's K/V at each sequence's current length;
  *   attend  single-query (GQA) attention over the cache, optionally with the
- *           append fused in.
+ *           append fused in;
+ * plus the legacy KV formats (flat packet, zero-padded batch, tensor-parallel
+ * head concatenation) and the same-GPU cross-process handoff (IPC).
  *
  * Conventions (all entry points):
  *   - Every pointer named *_dev or documented "device" is device memory on
@@ -50,7 +52,7 @@ enum hexkv_dtype {
 enum hexkv_kernel {
   HEXKV_KERNEL_AUTO = 0,
   HEXKV_KERNEL_VALU = 1, /* packed dot products on the vector ALUs     */
-  HEXKV_KERNEL_MFMA = 2  /* GQA group dot products on the matrix cores */
+  HEXKV_KERNEL_MFMA = 2  /* scores and P.V on the matrix cores           */
 };
 
 enum hexkv_status {

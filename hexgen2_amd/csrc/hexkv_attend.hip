@@ -849,12 +849,18 @@ static int kernel_group(int group) {
 }
 
 // Partition size: about (rows x head groups x positions) / 2048 positions,
-// as a power of two in [128, 1024], counting half of max_seqlen per row
+// as a power of two in [128, 512], counting half of max_seqlen per row
 // (ragged batches average about that).  Measured on MI355X (attention +
-// combine per layer): Llama-3-8B's shape (64 rows x 8 groups, lengths to 8K)
-// is fastest at 768-1024, Llama-2-7B's (8 x 32, to 2K) at 128-512, the
-// Llama-2-70B TP-8 share (32 x 1, to 4K) at 128-256 and TinyLlama (1 x 4,
-// 512) at 128.
+// combine per layer, interleaved A/B in one process): Llama-3-8B's shape
+// (64 rows x 8 groups, lengths to 8K) 165.3 us at 512, 166.5 at 768, 169.3 at
+// 1024, 168.1 at 384; the Llama-2-70B TP-8 share (32 x 1, to 4K) is fastest
+// at 128-256, TinyLlama (1 x 4, 512) at 64-256; Llama-2-7B (8 x 32, to 2K)
+// gets 256 (33.5 us; 1024 measured 32.4, 512 35.5 -- not monotonic, left
+// alone).  An evenly split persistent schedule (one wave of workgroups, each
+// an equal share of all positions, pieces merged after) was built and
+// measured slower on every one of these shapes (Llama-3-8B 172.5 vs 171.1 us,
+// the 70B TP-8 share 26.3 vs 15.9): at 512 positions the partitions already
+// balance the launch, and finer pieces only add partials to merge.
 static int choose_partition(const hexkv_attend_params *p) {
   if (p->partition > 0) return p->partition;
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
@@ -862,7 +868,7 @@ static int choose_partition(const hexkv_attend_params *p) {
   const int64_t half = std::max<int64_t>(1, (p->max_seqlen + 1) / 2);
   const int64_t want = rows * groups * half / 2048;
   int part = 128;
-  while (part < 1024 && part < want) part <<= 1;
+  while (part < 512 && part < want) part <<= 1;
   return part;
 }
 

@@ -116,9 +116,13 @@ def test_dominant_key_selects_value(device):
 def test_zero_length_rows_give_zeros(device):
     q, cache = make(3, 16, 8, 2, 64, torch.float16, 5, device)
     lens = torch.tensor([0, 5, 0], dtype=torch.int32, device=device)
-    out = ops.decode_attention(q, cache, max_seqlen=5, seqlens=lens)
+    out = torch.full_like(q, 9.0)  # stale values must be overwritten
+    ops.decode_attention(q, cache, max_seqlen=5, seqlens=lens, out=out)
     assert (out[0] == 0).all() and (out[2] == 0).all()
     check(out[1:2], q[1:2], cache[1:2], [5], torch.float16)
+    out = torch.full_like(q, 9.0)
+    ops.decode_attention(q, cache, max_seqlen=5, seqlens=torch.zeros(3, dtype=torch.int32, device=device), out=out)
+    assert (out == 0).all()
 
 
 FUSED = [(32, 8, 128, torch.bfloat16, "valu"), (32, 8, 128, torch.bfloat16, "mfma"),
@@ -194,6 +198,25 @@ def test_valu_and_mfma_agree(device):
     a = ops.decode_attention(q, cache, max_seqlen=3000, seqlens=lens, kernel="valu")
     b = ops.decode_attention(q, cache, max_seqlen=3000, seqlens=lens, kernel="mfma")
     torch.testing.assert_close(a.float(), b.float(), rtol=0, atol=8e-3)
+
+
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_many_ragged_rows(device, kernel):
+    # 300 rows of lengths 0..4000 (every 7th empty, one long): partitions of
+    # very different counts per row, most rows inside one partition
+    g = torch.Generator().manual_seed(15)
+    lens = torch.randint(0, 600, (300,), generator=g)
+    lens[::7] = 0
+    lens[5] = 4000
+    q, cache = make(300, 4001, 16, 2, 64, torch.float16, 15, device)
+    seqlens = lens.to(torch.int32).to(device)
+    live = [i for i, n in enumerate(lens.tolist()) if n > 0]
+    empty = [i for i, n in enumerate(lens.tolist()) if n == 0]
+    ref = oracle.attend(f64(q)[live], f64(cache)[live], [int(lens[i]) for i in live])
+    for partition in (0, 256):
+        out = ops.decode_attention(q, cache, max_seqlen=4000, seqlens=seqlens, kernel=kernel, partition=partition)
+        assert np.abs(f64(out)[live] - ref).max() <= TOL[torch.float16], partition
+        assert (out[empty] == 0).all(), partition
 
 
 def test_validation_errors(device):

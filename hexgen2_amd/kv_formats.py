@@ -232,15 +232,21 @@ def batch_key_value_memory_dicts(kv_memory_dicts_list: Sequence[Dict[int, torch.
     if any(t.dim() < 2 for t in first):
         raise ValueError("cache tensors must be [batch, positions, ...]")
     rest = tuple(first[0].shape[2:])
-    longest = max(t.shape[1] for t in first)
-    max_rows = longest if max_rows is None else int(max_rows)
     for key in keys:
         for i, d in enumerate(dicts):
             t = d[key]
-            if t.dim() < 2 or tuple(t.shape[2:]) != rest or t.shape[0] != first[i].shape[0] \
-                    or t.shape[1] != first[i].shape[1]:
+            if t.dim() < 2 or tuple(t.shape[2:]) != rest:
                 raise ValueError(f"request {i} layer {key}: shape {tuple(t.shape)} does not batch with "
-                                 f"{tuple(first[i].shape)} and rows {rest}")
+                                 f"rows of shape {rest}")
+    if any(d[key].shape[:2] != first[i].shape[:2] for key in keys for i, d in enumerate(dicts)):
+        # a request's sizes differ between layers: each key is padded to its
+        # own longest request (kv_cache_batch.py:14), one launch per key
+        out = {}
+        for key in keys:
+            out.update({key: batch_key_value_memory_dicts([{key: d[key]} for d in dicts], max_rows)[key]})
+        return out
+    longest = max(t.shape[1] for t in first)
+    max_rows = longest if max_rows is None else int(max_rows)
     seqs = sum(t.shape[0] for t in first)
     out = torch.empty((len(keys), seqs, max_rows, *rest), dtype=dtype, device=first[0].device)
     keep, blocks = [], []

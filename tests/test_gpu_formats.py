@@ -133,6 +133,17 @@ def test_batch_pad_ragged_strided_and_empty(device):
     assert kvf.batched_lengths(dicts) == [61, 61, 7, 0, 0, 64]
 
 
+def test_batch_pad_sizes_differing_between_layers(device):
+    # each key is padded to its own longest request, as the reference does
+    print("batch_pad per-key lengths", flush=True)
+    dicts = [{0: rand((1, 9, 2, 2, 16), torch.float16, 1, device), 1: rand((1, 4, 2, 2, 16), torch.float16, 2, device)},
+             {0: rand((2, 3, 2, 2, 16), torch.float16, 3, device), 1: rand((2, 11, 2, 2, 16), torch.float16, 4, device)}]
+    got = kvf.batch_key_value_memory_dicts(dicts)
+    for key, rows in ((0, 9), (1, 11)):
+        assert got[key].shape == (3, rows, 2, 2, 16)
+        np.testing.assert_array_equal(bits(got[key]), oracle.batch_pad([bits(d[key]) for d in dicts]))
+
+
 def test_batch_pad_four_byte_rows_and_many_spans(device):
     # 12-byte rows (fp16, 2 x 1 x 3) -> 4-byte vectors; 20 layers x 3 requests
     # x 2 spans > 32 spans per launch

@@ -174,7 +174,8 @@ def format_cases(device):
 
     g = torch.Generator(device=device).manual_seed(3)
     row = 2 * 8 * 128 * 2
-    spans_per_launch = 32  # kMaxSpans of the span-copy kernel
+    # Each case's layers are views of one stacked allocation, so the span
+    # engine folds them into one layer dimension: one launch per call.
     cases = []
     cache = torch.empty((32, 1, 8448, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
     layers = [cache[l, :, :8192] for l in range(32)]
@@ -184,14 +185,12 @@ def format_cases(device):
     lens = [int(x) for x in torch.randint(128, 4097, (8,), generator=torch.Generator().manual_seed(0))]
     bcache = torch.empty((32, 8, 4096, 2, 8, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
     dicts = [{l: bcache[l, i:i + 1, :n] for l in range(32)} for i, n in enumerate(lens)]
-    spans = 32 * sum(1 + (n < max(lens)) for n in lens)
     cases.append(("zero_pad_batch", lambda: kvf.batch_key_value_memory_dicts(dicts),
-                  32 * row * (sum(lens) + 8 * max(lens)), -(-spans // spans_per_launch), {"lens": lens}))
+                  32 * row * (sum(lens) + 8 * max(lens)), 1, {"lens": lens}))
 
     shards_t = torch.empty((8, 16, 8, 4096, 2, 1, 128), dtype=torch.bfloat16, device=device).normal_(generator=g)
     shards = [{l: shards_t[j, l] for l in range(16)} for j in range(8)]
-    cases.append(("tp_head_concat", lambda: kvf.concat_dicts(shards), 2 * shards_t.numel() * 2,
-                  -(-16 * 8 // spans_per_launch), {}))
+    cases.append(("tp_head_concat", lambda: kvf.concat_dicts(shards), 2 * shards_t.numel() * 2, 1, {}))
     return cases
 
 

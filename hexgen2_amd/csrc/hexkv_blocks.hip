@@ -29,8 +29,10 @@ struct Span {
   char *dst;
   int64_t width;                                   // bytes per row
   int64_t src_row, src_slice, dst_row, dst_slice;  // pitches, bytes
+  int64_t src_layer, dst_layer;                    // pitches between layers, bytes
   int64_t tile_cols;                               // bytes of one row per tile
   int32_t height;                                  // rows per slice
+  int32_t depth;                                   // slices per layer
   int32_t tile_rows;                               // rows per tile
   int32_t row_tiles;                               // tiles down one slice
   int32_t col_tiles;                               // tiles along one row
@@ -73,13 +75,15 @@ __global__ __launch_bounds__(kSpanThreads) void span_copy_kernel(const SpanArgs 
   const int ct = t % s.col_tiles;
   t /= s.col_tiles;
   const int rt = t % s.row_tiles;
-  const int64_t k = t / s.row_tiles;  // slice
+  t /= s.row_tiles;
+  const int64_t k = t % s.depth;  // slice
+  const int64_t m = t / s.depth;  // layer
   const int r0 = rt * s.tile_rows;
   const int r1 = min(s.height, r0 + s.tile_rows);
   const int64_t c0 = static_cast<int64_t>(ct) * s.tile_cols;
   const int64_t nv = (min(s.width, c0 + s.tile_cols) - c0) / static_cast<int64_t>(sizeof(V));
-  const char *src = s.src ? s.src + k * s.src_slice + c0 : nullptr;
-  char *dst = s.dst + k * s.dst_slice + c0;
+  const char *src = s.src ? s.src + m * s.src_layer + k * s.src_slice + c0 : nullptr;
+  char *dst = s.dst + m * s.dst_layer + k * s.dst_slice + c0;
   if (nv >= kSpanThreads) {
     for (int r = r0; r < r1; ++r)
       move_row<V>(src ? src + r * s.src_row : nullptr, dst + r * s.dst_row, nv);
@@ -109,15 +113,47 @@ __global__ __launch_bounds__(kSpanThreads) void span_copy_kernel(const SpanArgs 
 
 // ------------------------------------------------------------------ host ---
 
-// One span before tiling (all sizes in bytes).
+// One span before tiling (all sizes in bytes): `layers` copies of a
+// depth x height x width block, layer pitches apart.
 struct Move {
   const char *src;  // nullptr: zero fill
   char *dst;
   int64_t width, height, depth;
   int64_t src_row, src_slice, dst_row, dst_slice;
+  int64_t layers = 1, src_layer = 0, dst_layer = 0;
 };
 
-static int64_t move_bytes(const Move &m) { return m.width * m.height * m.depth; }
+static int64_t move_bytes(const Move &m) { return m.width * m.height * m.depth * m.layers; }
+
+static bool same_shape(const Move &a, const Move &b) {
+  return a.width == b.width && a.height == b.height && a.depth == b.depth && a.src_row == b.src_row &&
+         a.src_slice == b.src_slice && a.dst_row == b.dst_row && a.dst_slice == b.dst_slice &&
+         (a.src == nullptr) == (b.src == nullptr) && a.layers == 1 && b.layers == 1;
+}
+
+// `moves` holds n_layers groups of equally many moves, layer by layer.  When
+// move j of every layer has one shape and its source and destination advance
+// by fixed strides from layer to layer (the layers are views of one stacked
+// allocation), the n_layers copies become one move with a layer dimension:
+// one launch carries every layer.  Otherwise `moves` is left as it is.
+static void merge_layers(std::vector<Move> &moves, int n_layers) {
+  if (n_layers < 2 || moves.empty() || moves.size() % n_layers) return;
+  const size_t per = moves.size() / n_layers;
+  std::vector<Move> merged(moves.begin(), moves.begin() + per);
+  for (size_t j = 0; j < per; ++j) {
+    const Move &m0 = moves[j], &m1 = moves[per + j];
+    if (!same_shape(m0, m1)) return;
+    const int64_t ds = m0.src ? m1.src - m0.src : 0, dd = m1.dst - m0.dst;
+    for (int l = 2; l < n_layers; ++l) {
+      const Move &ml = moves[l * per + j];
+      if (!same_shape(m0, ml) || (m0.src && ml.src - m0.src != ds * l) || ml.dst - m0.dst != dd * l) return;
+    }
+    merged[j].layers = n_layers;
+    merged[j].src_layer = ds;
+    merged[j].dst_layer = dd;
+  }
+  moves.swap(merged);
+}
 
 // Merges dimensions that are contiguous on both sides, so the engine moves
 // the longest possible rows and tiles several short rows together.
@@ -169,6 +205,10 @@ static int run_moves(std::vector<Move> &moves, hipStream_t stream, const char *w
     if (m.height > 1) align |= static_cast<uint64_t>(m.dst_row) | static_cast<uint64_t>(m.src ? m.src_row : 0);
     if (m.depth > 1)
       align |= static_cast<uint64_t>(m.dst_slice) | static_cast<uint64_t>(m.src ? m.src_slice : 0);
+    if (m.layers > 1)
+      align |= static_cast<uint64_t>(m.dst_layer) | static_cast<uint64_t>(m.src ? m.src_layer : 0);
+    if (m.depth > INT32_MAX || m.layers * m.depth > INT32_MAX)
+      return fail(HEXKV_ERANGE, "%s: more than 2^31-1 slices in one block set", what);
     live.push_back(m);
   }
   if (live.empty()) return HEXKV_OK;
@@ -190,7 +230,10 @@ static int run_moves(std::vector<Move> &moves, hipStream_t stream, const char *w
       s.src_slice = m.src_slice;
       s.dst_row = m.dst_row;
       s.dst_slice = m.dst_slice;
+      s.src_layer = m.src_layer;
+      s.dst_layer = m.dst_layer;
       s.height = static_cast<int32_t>(m.height);
+      s.depth = static_cast<int32_t>(m.depth);
       int64_t col_tiles, row_tiles, tile_rows;
       if (m.width >= chunk) {
         s.tile_cols = chunk;
@@ -203,7 +246,7 @@ static int run_moves(std::vector<Move> &moves, hipStream_t stream, const char *w
         tile_rows = std::max<int64_t>(1, chunk / m.width);
         row_tiles = (m.height + tile_rows - 1) / tile_rows;
       }
-      const int64_t span_tiles = m.depth * row_tiles * col_tiles;
+      const int64_t span_tiles = m.layers * m.depth * row_tiles * col_tiles;
       if (span_tiles > INT32_MAX || tiles + span_tiles > INT32_MAX) {
         if (n == 0) return fail(HEXKV_ERANGE, "%s: block too large for one launch", what);
         break;  // next launch
@@ -267,6 +310,7 @@ extern "C" int hexkv_flat_concat(const hexkv_block *src, int n, void *dst, hexkv
                          b.height, b.depth, b.row_pitch, b.slice_pitch, b.width, b.width * b.height});
     off += bytes;
   }
+  merge_layers(moves, static_cast<int>(moves.size()));
   return run_moves(moves, static_cast<hipStream_t>(stream), what);
 }
 
@@ -316,6 +360,7 @@ extern "C" int hexkv_batch_pad(const hexkv_block *src, int n_layers, int n_req, 
       base += b.depth * seq_bytes;
     }
   }
+  merge_layers(moves, n_layers);
   return run_moves(moves, static_cast<hipStream_t>(stream), what);
 }
 
@@ -358,5 +403,6 @@ extern "C" int hexkv_head_concat(const hexkv_block *src, int n_layers, int n_sha
       col += b.width;
     }
   }
+  merge_layers(moves, n_layers);
   return run_moves(moves, static_cast<hipStream_t>(stream), what);
 }

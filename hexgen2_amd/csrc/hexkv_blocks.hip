@@ -7,7 +7,10 @@
 // of its own.  The host normalises each span (rows contiguous on both sides
 // merge into one long row; slices that follow each other become rows) and
 // cuts it into tiles of about one chunk of bytes: whole rows when rows are
-// short, row pieces when they are long.  One workgroup moves one tile with
+// short, row pieces when they are long.  When every layer's spans have one
+// shape and advance by fixed strides from layer to layer (layers that are
+// views of one stacked allocation), the layers fold into a fourth dimension
+// of each span and one launch moves them all.  One workgroup moves one tile with
 // nontemporal 16-byte loads and stores (narrower vectors only when an
 // address, pitch or width is not a multiple of 16), four in flight per lane;
 // short rows are spread over the workgroup several per pass, so a 256-byte

@@ -43,8 +43,9 @@ def log(msg):
 class Job:
     """Device buffers of one workload and the timed job pass."""
 
-    def __init__(self, w, device):
+    def __init__(self, w, device, kernel="auto"):
         self.w = w
+        self.kernel = kernel
         L, B, S = w.layers, w.batch, w.capacity
         shape = (L, B, S, 2, w.kv_heads, w.head_dim)
         g = torch.Generator(device=device).manual_seed(w.seed + 1)
@@ -61,7 +62,8 @@ class Job:
         self.max_len = max(w.lens)
         self.plan = ops.AttendPlan(self.q[0], self.decode_layers[0], self.out,
                                    max_seqlens=[self.max_len + t + 1 for t in range(w.decode_steps)],
-                                   seqlens=self.seqlens, kv_new=self.kv_new[0])
+                                   seqlens=self.seqlens, kv_new=self.kv_new[0], kernel=kernel)
+        self.kernel_name = ops.attend_kernel(self.q[0], self.decode_layers[0], kernel)
         self.positions = self.seqlens.clone()
         self.graph = None
         torch.cuda.synchronize()
@@ -71,7 +73,7 @@ class Job:
         w = self.w
         self.graph = ops.DecodeStepGraph(list(self.q.unbind(0)), self.decode_layers, [self.out] * w.layers,
                                          list(self.kv_new.unbind(0)), self.positions,
-                                         self.max_len + w.decode_steps)
+                                         self.max_len + w.decode_steps, kernel=self.kernel)
 
     def run_graph(self, events):
         """pack -> unpack -> decode steps replayed from the captured graph."""
@@ -279,6 +281,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--no-formats", action="store_true", help="skip the legacy-format figures")
+    ap.add_argument("--kernel", default="auto", choices=("auto", "valu", "mfma"),
+                    help="attention kernel (auto: the library's choice for the workload)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the short dispatch sequence for hardware-counter runs")
     args = ap.parse_args()
@@ -289,8 +293,8 @@ def main():
     device = torch.device("cuda", 0)
     w = workload(args.workload)
     log(f"workload {w.describe()}")
-    job = Job(w, device)
-    log("buffers ready")
+    job = Job(w, device, args.kernel)
+    log(f"buffers ready; attention kernel {job.kernel_name}")
     if args.traffic_probe:
         job.traffic_probe()
         del job
@@ -349,7 +353,8 @@ def main():
         "vs_baseline": None,
         "dtype": str(w.dtype).split(".")[-1].replace("bfloat16", "bf16").replace("float16", "fp16"),
         "data": "synthetic (seeded N(0,1) K/V, seeded ragged lengths)",
-        "config": {**w.describe(), "parallelism": "single GPU (prefill and decode share it)"},
+        "config": {**w.describe(), "attention_kernel": job.kernel_name,
+                   "parallelism": "single GPU (prefill and decode share it)"},
         "pack_unpack_ms": round(pu_ms, 3),
         "pack_unpack_hbm_frac": round(pu_gbs / HBM_PEAK_GBS, 4),
         "pack_ms": round(statistics.median(pack_times), 3),
@@ -357,7 +362,7 @@ def main():
         "decode_gbs": round(decode_gbs, 1),
         "decode_hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "attend_kernel + combine_kernel (fused append+attend, one layer)",
+            "kernel": f"attend_{job.kernel_name}_kernel + combine_kernel (fused append+attend, one layer)",
             "bound": "hbm",
             "achieved": round(launch_bytes / (attend_us * 1e-6) / 1e9, 1),
             "peak": HBM_PEAK_GBS,

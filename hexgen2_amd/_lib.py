@@ -19,7 +19,7 @@ MAX_SEQS_PER_LAUNCH = 256
 
 # Every symbol the header declares; tests check the library exports them all.
 EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "hexkv_append",
-           "hexkv_attend_workspace_bytes", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
+           "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
            "hexkv_ipc_dlpack")
 
@@ -81,6 +81,8 @@ def load() -> ctypes.CDLL:
     lib.hexkv_append.argtypes = [vp, vp, ci, i64, i64, i64, vp, i32, vp]
     lib.hexkv_attend_workspace_bytes.restype = ctypes.c_size_t
     lib.hexkv_attend_workspace_bytes.argtypes = [ctypes.POINTER(AttendParams)]
+    lib.hexkv_attend_kernel.restype = ctypes.c_int
+    lib.hexkv_attend_kernel.argtypes = [ctypes.POINTER(AttendParams)]
     lib.hexkv_attend.restype = ci
     lib.hexkv_attend.argtypes = [ctypes.POINTER(AttendParams), vp, ctypes.c_size_t, vp]
     blocks = ctypes.POINTER(Block)

@@ -1000,6 +1000,16 @@ extern "C" size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p) {
   return workspace_bytes(p, choose_partition(p));
 }
 
+extern "C" int hexkv_attend_kernel(const hexkv_attend_params *p) {
+  using namespace hexkv;
+  clear_error();
+  if (!p || p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads != 0)
+    return fail(HEXKV_EINVAL, "hexkv_attend_kernel: bad q_heads/kv_heads");
+  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_MFMA)
+    return fail(HEXKV_EINVAL, "hexkv_attend_kernel: unknown kernel %d", p->kernel);
+  return use_mfma(p, kernel_group(p->q_heads / p->kv_heads)) ? HEXKV_KERNEL_MFMA : HEXKV_KERNEL_VALU;
+}
+
 extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_t ws_bytes,
                             hexkv_stream_t stream) {
   using namespace hexkv;

@@ -243,6 +243,15 @@ def attend_workspace_bytes(q: torch.Tensor, cache: torch.Tensor, max_seqlen: int
     return int(_lib.load().hexkv_attend_workspace_bytes(ctypes.byref(p)))
 
 
+def attend_kernel(q: torch.Tensor, cache: torch.Tensor, kernel: str = "auto") -> str:
+    """Name of the kernel ("valu" or "mfma") ``decode_attention`` runs for
+    this geometry and ``kernel`` choice."""
+    p = _attend_params(q, cache, q, None, 1, 1, None, False, None, 0, kernel)
+    rc = int(_lib.load().hexkv_attend_kernel(ctypes.byref(p)))
+    _lib.check(min(rc, 0), "hexkv_attend_kernel")
+    return {v: k for k, v in _lib.KERNELS.items()}[rc]
+
+
 def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
                      seqlens: Optional[torch.Tensor] = None, seqlen_bias: int = 0,
                      kv_new: Optional[torch.Tensor] = None, causal: bool = False,

@@ -180,6 +180,12 @@ typedef struct hexkv_attend_params {
  * outputs of the split-K merge); calls sharing one must not overlap. */
 size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p);
 
+/* The kernel hexkv_attend runs for these parameters, HEXKV_KERNEL_VALU or
+ * HEXKV_KERNEL_MFMA (HEXKV_KERNEL_AUTO resolved by head group, head_dim and
+ * dtype), or a negative error code.  No counterpart in the reference: it
+ * lets profiling and benchmarks name the kernel they measure. */
+int hexkv_attend_kernel(const hexkv_attend_params *p);
+
 /*
  * Single-query GQA attention over the cache, optionally appending first:
  *   out[b,t,h] = sum_s softmax_s(q[b,t,h] . K[b,s,h/g] * scale) V[b,s,h/g]

@@ -118,3 +118,27 @@ def test_cpu_tensors_are_rejected_loudly():
         ops.pack_live([cache], [2])
     with pytest.raises(ValueError, match="no CPU fallback"):
         ops.decode_attention(torch.zeros((1, 1, 2, 8)), cache, max_seqlen=2, seqlen_bias=2)
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel,expect", [
+    (32, 8, 128, torch.bfloat16, "auto", "valu"),    # Llama-3-8B: group 4
+    (8, 1, 128, torch.bfloat16, "auto", "mfma"),     # Llama-2-70B TP-8 share: group 8
+    (32, 4, 64, torch.float16, "auto", "mfma"),      # TinyLlama: group 8, head_dim 64
+    (32, 32, 128, torch.float16, "auto", "valu"),    # Llama-2-7B: group 1
+    (8, 1, 128, torch.float32, "auto", "valu"),      # fp32 never takes the matrix cores
+    (8, 1, 32, torch.float16, "auto", "valu"),       # head_dim below 64
+    (8, 1, 128, torch.bfloat16, "valu", "valu"),
+    (32, 8, 128, torch.bfloat16, "mfma", "mfma")])
+def test_attend_kernel_choice(hq, hkv, d, dtype, kernel, expect):
+    """hexkv_attend_kernel resolves the kernel choice from geometry alone
+    (no device memory is touched)."""
+    q = torch.empty((2, 1, hq, d), dtype=dtype)
+    cache = torch.empty((2, 16, 2, hkv, d), dtype=dtype)
+    assert ops.attend_kernel(q, cache, kernel) == expect
+
+
+def test_attend_kernel_rejects_bad_geometry():
+    p = _lib.AttendParams()
+    p.q_heads, p.kv_heads = 6, 4
+    assert _lib.load().hexkv_attend_kernel(ctypes.byref(p)) == _lib.HEXKV_EINVAL
+    assert b"q_heads" in _lib.load().hexkv_last_error()

@@ -21,7 +21,7 @@ MAX_SEQS_PER_LAUNCH = 256
 EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "hexkv_append",
            "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
-           "hexkv_ipc_dlpack")
+           "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend")
 
 
 class AttendParams(ctypes.Structure):
@@ -37,6 +37,21 @@ class AttendParams(ctypes.Structure):
         ("out", ctypes.c_void_p), ("out_batch_stride", ctypes.c_int64), ("out_row_stride", ctypes.c_int64),
         ("seqlens_dev", ctypes.c_void_p), ("seqlen_bias", ctypes.c_int32), ("max_seqlen", ctypes.c_int32),
         ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int), ("kernel", ctypes.c_int),
+    ]
+
+
+class FtAttendParams(ctypes.Structure):
+    """Mirror of ``hexkv_ft_attend_params``."""
+    _fields_ = [
+        ("dtype", ctypes.c_int), ("batch", ctypes.c_int), ("q_heads", ctypes.c_int),
+        ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("softmax_scale", ctypes.c_float),
+        ("q", ctypes.c_void_p), ("q_batch_stride", ctypes.c_int64),
+        ("k_new", ctypes.c_void_p), ("v_new", ctypes.c_void_p), ("new_batch_stride", ctypes.c_int64),
+        ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p), ("capacity", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("out_batch_stride", ctypes.c_int64),
+        ("positions_dev", ctypes.c_void_p), ("position_bias", ctypes.c_int32), ("max_position", ctypes.c_int32),
+        ("rotary_dim", ctypes.c_int), ("rotary_base", ctypes.c_float), ("rotary_neox", ctypes.c_int),
+        ("partition", ctypes.c_int),
     ]
 
 
@@ -101,6 +116,12 @@ def load() -> ctypes.CDLL:
     lib.hexkv_ipc_close.argtypes = [vp]
     lib.hexkv_ipc_dlpack.restype = vp
     lib.hexkv_ipc_dlpack.argtypes = [vp, u64, ci, ctypes.POINTER(i64), ci, ci, ci]
+    lib.hexkv_ft_store.restype = ci
+    lib.hexkv_ft_store.argtypes = [vp, i64, i64, i64, vp, vp, ci, ci, i64, ci, ci, ci, vp]
+    lib.hexkv_ft_attend_workspace_bytes.restype = ctypes.c_size_t
+    lib.hexkv_ft_attend_workspace_bytes.argtypes = [ctypes.POINTER(FtAttendParams)]
+    lib.hexkv_ft_attend.restype = ci
+    lib.hexkv_ft_attend.argtypes = [ctypes.POINTER(FtAttendParams), vp, ctypes.c_size_t, vp]
     _lib = lib
     return lib
 

@@ -1,5 +1,7 @@
 // Single-query GQA decode attention over the KV cache, with optional fused
-// append of the new token's K/V (hexkv_attend in hexkv.h).
+// append of the new token's K/V (hexkv_attend in hexkv.h), and the same over
+// the FasterTransformer cache layouts with rotary embedding (hexkv_ft_attend:
+// the VALU kernel with FT addressing and a rotary prologue).
 //
 // Work decomposition (split-K, "flash-decoding"):
 //   grid = (partition, q-head group, query row).  A workgroup (4 waves) owns
@@ -74,6 +76,19 @@ struct AttendArgs {
   float scale_log2;    // softmax_scale * log2(e), > 0
   float *ws_o;         // [rows][q_heads][max_parts][D]
   float *ws_ml;        // [rows][q_heads][max_parts][2]
+  // FasterTransformer cache layouts (hexkv_ft_attend only): K is
+  // [batch][kv_heads][D / pack][capacity][pack] (one 16-byte chunk of D per
+  // position), V is [batch][kv_heads][capacity][D]; strides in bytes.  The
+  // new row's K comes from kv_new, its V from v_new, both [batch][kv_heads][D]
+  // rows new_bs elements apart, and q and k are rotated first when rot_dim > 0.
+  const void *k_ft, *v_ft;
+  int64_t k_ft_batch, k_ft_head, k_ft_chunk;
+  int64_t v_ft_batch, v_ft_head;
+  const void *v_new;
+  int64_t new_bs;
+  int32_t rot_dim;      // leading dims of each head that rotate (0: none)
+  int32_t rot_neox;     // 1: pairs (i, i + rot_dim / 2); 0: pairs (2i, 2i + 1)
+  double rot_log2_base;  // log2 of the rotary base
 };
 
 // Number of keys query row (b, t) attends to; *pos_new = cache position of the
@@ -214,9 +229,58 @@ __device__ __forceinline__ void lazy_rescale(const float (&mt)[G], float (&m)[G]
   }
 }
 
+// 16 bytes of T rounded from VEC floats.
+template <typename T>
+__device__ __forceinline__ u32x4 pack16(const float *f) {
+  constexpr int VEC = 16 / static_cast<int>(sizeof(T));
+  T t[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) t[i] = Elem<T>::from_float(f[i]);
+  u32x4 r;
+  __builtin_memcpy(&r, t, 16);
+  return r;
+}
+
+// FT layout prologue: the workgroup's G query heads (sq, G x D) and, for the
+// workgroup that attends the new row, its K (skn, D) as fp32 in LDS, rotated
+// in place at the new row's position when rot_dim > 0: pair (x0, x1) of
+// dimension pair j turns by pos * base^(-2j / rot_dim) radians.  The angle
+// and its sine and cosine are evaluated in fp64 (an fp32 angle is off by
+// ~pos * 2^-24 radians, 6e-5 at position 1000); the turn itself is fp32.
+// The caller rounds both back to T when it packs them, as the reference
+// kernel does.
+template <typename T, int D, int G>
+__device__ __forceinline__ void ft_prologue(const AttendArgs &a, const Work &w, float *sq, float *skn) {
+  const T *q = static_cast<const T *>(a.q) + w.b * a.q_bs + w.qh0 * D;
+  for (int i = threadIdx.x; i < G * D; i += kAttThreads) sq[i] = static_cast<float>(q[i]);
+  if (w.has_new) {
+    const T *k = static_cast<const T *>(a.kv_new) + w.b * a.new_bs + static_cast<int64_t>(w.hk) * D;
+    for (int i = threadIdx.x; i < D; i += kAttThreads) skn[i] = static_cast<float>(k[i]);
+  }
+  __syncthreads();
+  const int half = a.rot_dim / 2;
+  if (half > 0) {
+    const int pos = w.pos_new;
+    const int vecs = w.has_new ? G + 1 : G;
+    for (int i = threadIdx.x; i < vecs * half; i += kAttThreads) {
+      const int g = i / half, j = i - g * half;
+      float *x = g < G ? sq + g * D : skn;
+      const int i0 = a.rot_neox ? j : 2 * j, i1 = a.rot_neox ? j + half : 2 * j + 1;
+      const double theta = static_cast<double>(pos) * exp2(-static_cast<double>(2 * j) / a.rot_dim * a.rot_log2_base);
+      double sd, cd;
+      sincos(theta, &sd, &cd);
+      const float sn = static_cast<float>(sd), cs = static_cast<float>(cd);
+      const float x0 = x[i0], x1 = x[i1];
+      x[i0] = x0 * cs - x1 * sn;
+      x[i1] = x0 * sn + x1 * cs;
+    }
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------------------- VALU path ---
 
-template <typename T, int D, int G, int U, bool PF = true>
+template <typename T, int D, int G, int U, bool PF = true, bool FT = false>
 __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendArgs a) {
   using E = Elem<T>;
   using L = Lanes<T, D>;
@@ -224,6 +288,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   constexpr int STEP = NG * U;  // positions per workgroup iteration
   __shared__ float s_acc[kAttWaves][G][D];
   __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
+  __shared__ float s_kn[FT ? D : 1];
   Work w;
   if (!begin_work<T, D, G>(a, w)) return;
 
@@ -231,21 +296,47 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   const int sub = lane % LPP, gid = wave * GPW + lane / LPP;
   const float scale = a.scale_log2;
 
-  const T *qrow = static_cast<const T *>(a.q) + w.b * a.q_bs + w.t * a.q_rs + w.qh0 * D + sub * EPL;
   u32x4 qv[G][NV];
+  if constexpr (FT) {
+    ft_prologue<T, D, G>(a, w, &s_acc[0][0][0], s_kn);
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int v = 0; v < NV; ++v) qv[g][v] = *reinterpret_cast<const u32x4 *>(qrow + g * D + v * VEC);
+      for (int v = 0; v < NV; ++v) qv[g][v] = pack16<T>(&s_acc[0][g][sub * EPL + v * VEC]);
+    __syncthreads();  // every wave holds its query before s_acc is written again
+  } else {
+    const T *qrow = static_cast<const T *>(a.q) + w.b * a.q_bs + w.t * a.q_rs + w.qh0 * D + sub * EPL;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) qv[g][v] = *reinterpret_cast<const u32x4 *>(qrow + g * D + v * VEC);
+  }
 
   // Uniform bases of this sequence's K and V head slices; lane offsets are
-  // 32-bit (the host checks capacity * position stride fits).
-  const char *kseq = static_cast<const char *>(a.cache) +
-                     (w.b * a.c_bs + static_cast<int64_t>(w.hk) * D) * static_cast<int64_t>(sizeof(T));
-  const char *vseq = kseq + a.c_kv * static_cast<int64_t>(sizeof(T));
-  const uint32_t row_bytes = static_cast<uint32_t>(a.c_ps * sizeof(T));
+  // 32-bit (the host checks capacity * position stride fits).  In the
+  // standard layout K and V of a position share one offset; in the FT layout
+  // a K position is one 16-byte chunk (the lane's chunks kchunk apart) and a
+  // V position one head row.
+  const char *kseq, *vseq;
+  uint32_t row_bytes, vrow_bytes, kchunk, klane;
   const uint32_t lane_off = static_cast<uint32_t>(sub * EPL * sizeof(T));
-  const uint32_t lane_base = static_cast<uint32_t>(w.p0 + gid) * row_bytes + lane_off;
+  if constexpr (FT) {
+    kseq = static_cast<const char *>(a.k_ft) + w.b * a.k_ft_batch + w.hk * a.k_ft_head;
+    vseq = static_cast<const char *>(a.v_ft) + w.b * a.v_ft_batch + w.hk * a.v_ft_head;
+    row_bytes = 16;
+    vrow_bytes = static_cast<uint32_t>(D * sizeof(T));
+    kchunk = static_cast<uint32_t>(a.k_ft_chunk);
+    klane = static_cast<uint32_t>(sub * NV) * kchunk;
+  } else {
+    kseq = static_cast<const char *>(a.cache) +
+           (w.b * a.c_bs + static_cast<int64_t>(w.hk) * D) * static_cast<int64_t>(sizeof(T));
+    vseq = kseq + a.c_kv * static_cast<int64_t>(sizeof(T));
+    row_bytes = vrow_bytes = static_cast<uint32_t>(a.c_ps * sizeof(T));
+    kchunk = 16;
+    klane = lane_off;
+  }
+  const uint32_t lane_base = static_cast<uint32_t>(w.p0 + gid) * row_bytes + klane;
+  const uint32_t vlane_base = static_cast<uint32_t>(w.p0 + gid) * vrow_bytes + lane_off;
 
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -264,17 +355,20 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
     constexpr bool TAIL = decltype(tail)::value;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      uint32_t off;
+      uint32_t off, voff;
       if constexpr (TAIL) {
         const int p = min(i0 + u * NG + gid, w.n_cache - 1);
-        off = static_cast<uint32_t>(w.p0 + p) * row_bytes + lane_off;
+        off = static_cast<uint32_t>(w.p0 + p) * row_bytes + klane;
+        if constexpr (FT) voff = static_cast<uint32_t>(w.p0 + p) * vrow_bytes + lane_off;
       } else {
         off = lane_base + static_cast<uint32_t>(i0 + u * NG) * row_bytes;
+        if constexpr (FT) voff = vlane_base + static_cast<uint32_t>(i0 + u * NG) * vrow_bytes;
       }
+      if constexpr (!FT) voff = off;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        kr[u][v] = load16(kseq, off + v * 16);
-        vr[u][v] = load16(vseq, off + v * 16);
+        kr[u][v] = load16(kseq, off + v * kchunk);
+        vr[u][v] = load16(vseq, voff + v * 16);
       }
     }
   };
@@ -361,14 +455,24 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   if (w.has_new) {
     // The new row: attended by lane group 0 from kv_new, written to the cache
     // by that lane group of the writer workgroup.
-    const char *knew = static_cast<const char *>(a.kv_new) +
-                       ((static_cast<int64_t>(w.b) * 2 * a.kv_heads + w.hk) * D) * static_cast<int64_t>(sizeof(T));
-    const char *vnew = knew + static_cast<int64_t>(a.kv_heads) * D * sizeof(T);
     u32x4 kn[NV], vn[NV];
+    if constexpr (FT) {
+      const char *vnew = static_cast<const char *>(a.v_new) +
+                         (w.b * a.new_bs + static_cast<int64_t>(w.hk) * D) * static_cast<int64_t>(sizeof(T));
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      kn[v] = *reinterpret_cast<const u32x4 *>(knew + lane_off + v * 16);
-      vn[v] = *reinterpret_cast<const u32x4 *>(vnew + lane_off + v * 16);
+      for (int v = 0; v < NV; ++v) {
+        kn[v] = pack16<T>(s_kn + sub * EPL + v * VEC);
+        vn[v] = *reinterpret_cast<const u32x4 *>(vnew + lane_off + v * 16);
+      }
+    } else {
+      const char *knew = static_cast<const char *>(a.kv_new) +
+                         ((static_cast<int64_t>(w.b) * 2 * a.kv_heads + w.hk) * D) * static_cast<int64_t>(sizeof(T));
+      const char *vnew = knew + static_cast<int64_t>(a.kv_heads) * D * sizeof(T);
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        kn[v] = *reinterpret_cast<const u32x4 *>(knew + lane_off + v * 16);
+        vn[v] = *reinterpret_cast<const u32x4 *>(vnew + lane_off + v * 16);
+      }
     }
     float sc[G], mt[G];
 #pragma unroll
@@ -391,11 +495,12 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
       for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
     }
     if (w.writer && gid == 0) {
-      const uint32_t off = static_cast<uint32_t>(w.pos_new) * row_bytes + lane_off;
+      const uint32_t off = static_cast<uint32_t>(w.pos_new) * row_bytes + klane;
+      const uint32_t voff = static_cast<uint32_t>(w.pos_new) * vrow_bytes + lane_off;
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        *reinterpret_cast<u32x4 *>(const_cast<char *>(kseq) + off + v * 16) = kn[v];
-        *reinterpret_cast<u32x4 *>(const_cast<char *>(vseq) + off + v * 16) = vn[v];
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(kseq) + off + v * kchunk) = kn[v];
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(vseq) + voff + v * 16) = vn[v];
       }
     }
   }
@@ -950,10 +1055,15 @@ static bool use_mfma(const hexkv_attend_params *p, int G) {
   return p->dtype != HEXKV_F32 && p->head_dim >= 64 && G >= 8;
 }
 
+// Which attention kernel a launch runs.
+enum LaunchKind { kLaunchValu = 0, kLaunchMfma = 1, kLaunchFt = 2 };
+
 template <typename T, int D, int G>
-static void launch(const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
-  if constexpr (sizeof(T) == 2 && D >= 64) {
-    if (mfma) attend_mfma_kernel<T, D, G><<<grid, kAttThreads, 0, s>>>(a);
+static void launch(const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
+  if (kind == kLaunchFt) {
+    attend_valu_kernel<T, D, G, slots<T, D, G>(), true, true><<<grid, kAttThreads, 0, s>>>(a);
+  } else if constexpr (sizeof(T) == 2 && D >= 64) {
+    if (kind == kLaunchMfma) attend_mfma_kernel<T, D, G><<<grid, kAttThreads, 0, s>>>(a);
     else attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
   } else {
     attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
@@ -967,25 +1077,25 @@ static void launch(const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
 }
 
 template <typename T, int D>
-static int dispatch_g(int G, const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
+static int dispatch_g(int G, const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
   switch (G) {
-    case 1: launch<T, D, 1>(a, grid, mfma, s); break;
-    case 2: launch<T, D, 2>(a, grid, mfma, s); break;
-    case 4: launch<T, D, 4>(a, grid, mfma, s); break;
-    case 8: launch<T, D, 8>(a, grid, mfma, s); break;
+    case 1: launch<T, D, 1>(a, grid, kind, s); break;
+    case 2: launch<T, D, 2>(a, grid, kind, s); break;
+    case 4: launch<T, D, 4>(a, grid, kind, s); break;
+    case 8: launch<T, D, 8>(a, grid, kind, s); break;
     default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: group %d", G);
   }
   return HEXKV_OK;
 }
 
 template <typename T>
-static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, bool mfma, hipStream_t s) {
+static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
   switch (D) {
-    case 16: return dispatch_g<T, 16>(G, a, grid, mfma, s);
-    case 32: return dispatch_g<T, 32>(G, a, grid, mfma, s);
-    case 64: return dispatch_g<T, 64>(G, a, grid, mfma, s);
-    case 128: return dispatch_g<T, 128>(G, a, grid, mfma, s);
-    case 256: return dispatch_g<T, 256>(G, a, grid, mfma, s);
+    case 16: return dispatch_g<T, 16>(G, a, grid, kind, s);
+    case 32: return dispatch_g<T, 32>(G, a, grid, kind, s);
+    case 64: return dispatch_g<T, 64>(G, a, grid, kind, s);
+    case 128: return dispatch_g<T, 128>(G, a, grid, kind, s);
+    case 256: return dispatch_g<T, 256>(G, a, grid, kind, s);
     default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: head_dim %d", D);
   }
 }
@@ -1027,7 +1137,7 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
     return fail(HEXKV_EINVAL, "hexkv_attend: workspace must be 16-byte aligned");
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
 
-  AttendArgs a;
+  AttendArgs a{};
   a.q = p->q;
   a.q_bs = p->q_batch_stride;
   a.q_rs = p->q_row_stride;
@@ -1066,12 +1176,148 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
   const unsigned grid_x = static_cast<unsigned>(max_parts | 1);
   dim3 grid(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool mfma = use_mfma(p, G);
+  const int kind = use_mfma(p, G) ? kLaunchMfma : kLaunchValu;
   switch (p->dtype) {
-    case HEXKV_BF16: rc = dispatch_d<__bf16>(p->head_dim, G, a, grid, mfma, s); break;
-    case HEXKV_F16: rc = dispatch_d<_Float16>(p->head_dim, G, a, grid, mfma, s); break;
-    default: rc = dispatch_d<float>(p->head_dim, G, a, grid, mfma, s); break;
+    case HEXKV_BF16: rc = dispatch_d<__bf16>(p->head_dim, G, a, grid, kind, s); break;
+    case HEXKV_F16: rc = dispatch_d<_Float16>(p->head_dim, G, a, grid, kind, s); break;
+    default: rc = dispatch_d<float>(p->head_dim, G, a, grid, kind, s); break;
   }
   if (rc != HEXKV_OK) return rc;
   return check_launch("hexkv_attend");
+}
+
+// ------------------------------------------------------------ FT layout ---
+
+namespace hexkv {
+
+// The geometry of an FT call as hexkv_attend parameters (q_len 1, the VALU
+// kernel, keys up to max_position + 1): partition, workspace and grid follow
+// the same rules.
+static hexkv_attend_params ft_geometry(const hexkv_ft_attend_params *p) {
+  hexkv_attend_params g{};
+  g.dtype = p->dtype;
+  g.batch = p->batch;
+  g.q_len = 1;
+  g.q_heads = p->q_heads;
+  g.kv_heads = p->kv_heads;
+  g.head_dim = p->head_dim;
+  g.softmax_scale = p->softmax_scale;
+  g.capacity = p->capacity;
+  g.max_seqlen = p->max_position + 1;
+  g.partition = p->partition;
+  g.kernel = HEXKV_KERNEL_VALU;
+  return g;
+}
+
+static int validate_ft(const hexkv_ft_attend_params *p) {
+  const char *what = "hexkv_ft_attend";
+  if (!p) return fail(HEXKV_EINVAL, "%s: null params", what);
+  if (p->dtype != HEXKV_F16 && p->dtype != HEXKV_BF16 && p->dtype != HEXKV_F32)
+    return fail(HEXKV_EINVAL, "%s: unknown dtype %d", what, p->dtype);
+  if (p->batch < 0 || p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads != 0)
+    return fail(HEXKV_EINVAL, "%s: bad batch or head counts", what);
+  const int d = p->head_dim;
+  if (d != 16 && d != 32 && d != 64 && d != 128 && d != 256)
+    return fail(HEXKV_EUNSUPPORTED, "%s: head_dim %d (compiled: 16, 32, 64, 128, 256)", what, d);
+  if (p->batch > 65535) return fail(HEXKV_EINVAL, "%s: batch above 65535", what);
+  if (p->capacity < 1 || p->max_position < 0 || p->max_position >= p->capacity)
+    return fail(HEXKV_ERANGE, "%s: max_position %d outside [0, capacity %lld)", what, p->max_position,
+                static_cast<long long>(p->capacity));
+  if (p->rotary_dim < 0 || p->rotary_dim > d || p->rotary_dim % 2 != 0)
+    return fail(HEXKV_EINVAL, "%s: rotary_dim %d must be even and at most head_dim", what, p->rotary_dim);
+  if (p->rotary_dim > 0 && !(p->rotary_base > 0.f && p->rotary_base < 3.0e38f))
+    return fail(HEXKV_EINVAL, "%s: rotary_base must be positive and finite", what);
+  if (!(p->softmax_scale > 0.f) || p->softmax_scale > 3.0e38f)
+    return fail(HEXKV_EINVAL, "%s: softmax_scale must be positive and finite", what);
+  if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > 4096)))
+    return fail(HEXKV_EINVAL, "%s: partition must be 0 or a multiple of 64 up to 4096", what);
+  if (p->batch == 0) return HEXKV_OK;
+  if (!p->q || !p->k_new || !p->v_new || !p->k_cache || !p->v_cache || !p->out)
+    return fail(HEXKV_EINVAL, "%s: null tensor", what);
+  const int es = elem_size(p->dtype), vec = 16 / es;
+  if (!aligned16(p->q) || !aligned16(p->k_new) || !aligned16(p->v_new) || !aligned16(p->k_cache) ||
+      !aligned16(p->v_cache))
+    return fail(HEXKV_EINVAL, "%s: q, k_new, v_new and the caches must be 16-byte aligned", what);
+  if (p->q_batch_stride % vec || p->new_batch_stride % vec)
+    return fail(HEXKV_EINVAL, "%s: strides must be multiples of 16 bytes", what);
+  if ((reinterpret_cast<uintptr_t>(p->out) & (es - 1)) != 0) return fail(HEXKV_EINVAL, "%s: out misaligned", what);
+  // K chunks and V rows of one (sequence, head) are addressed by 32-bit offsets.
+  if (p->capacity > (INT64_C(1) << 31) / (static_cast<int64_t>(d) * es))
+    return fail(HEXKV_EUNSUPPORTED, "%s: capacity * head_dim * element above 2 GiB", what);
+  return HEXKV_OK;
+}
+
+}  // namespace hexkv
+
+extern "C" size_t hexkv_ft_attend_workspace_bytes(const hexkv_ft_attend_params *p) {
+  using namespace hexkv;
+  if (!p || p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads || p->batch < 0 ||
+      p->max_position < 0)
+    return 0;
+  const hexkv_attend_params g = ft_geometry(p);
+  return workspace_bytes(&g, choose_partition(&g));
+}
+
+extern "C" int hexkv_ft_attend(const hexkv_ft_attend_params *p, void *workspace, size_t ws_bytes,
+                               hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  int rc = validate_ft(p);
+  if (rc != HEXKV_OK || p->batch == 0) return rc;
+  const hexkv_attend_params g = ft_geometry(p);
+  const int part = choose_partition(&g);
+  const int G = kernel_group(p->q_heads / p->kv_heads);
+  const int64_t max_parts = max_parts_of(&g, part);
+  const size_t need = workspace_bytes(&g, part);
+  if (need > 0 && (!workspace || ws_bytes < need))
+    return fail(HEXKV_EWORKSPACE, "hexkv_ft_attend: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+  if (need > 0 && !aligned16(workspace))
+    return fail(HEXKV_EINVAL, "hexkv_ft_attend: workspace must be 16-byte aligned");
+  const int64_t rows = p->batch;
+  const int64_t es = elem_size(p->dtype), d = p->head_dim, cap = p->capacity;
+
+  AttendArgs a{};
+  a.q = p->q;
+  a.q_bs = p->q_batch_stride;
+  a.out = p->out;
+  a.o_bs = p->out_batch_stride;
+  a.kv_new = p->k_new;
+  a.v_new = p->v_new;
+  a.new_bs = p->new_batch_stride;
+  a.seqlens = p->positions_dev;
+  a.bias = p->position_bias;
+  a.q_len = 1;
+  a.q_heads = p->q_heads;
+  a.kv_heads = p->kv_heads;
+  a.group = p->q_heads / p->kv_heads;
+  a.part = part;
+  a.max_parts = static_cast<int32_t>(max_parts);
+  a.max_seqlen = p->max_position + 1;
+  a.capacity = cap;
+  a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
+  if (need > 0) {
+    a.ws_o = static_cast<float *>(workspace);
+    a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
+  }
+  a.k_ft = p->k_cache;
+  a.v_ft = p->v_cache;
+  a.k_ft_head = d * cap * es;  // D / pack chunks of capacity x 16 bytes
+  a.k_ft_batch = p->kv_heads * a.k_ft_head;
+  a.k_ft_chunk = cap * 16;
+  a.v_ft_head = cap * d * es;
+  a.v_ft_batch = p->kv_heads * a.v_ft_head;
+  a.rot_dim = p->rotary_dim;
+  a.rot_neox = p->rotary_neox ? 1 : 0;
+  a.rot_log2_base = p->rotary_dim > 0 ? log2(static_cast<double>(p->rotary_base)) : 0.0;
+
+  const unsigned grid_x = static_cast<unsigned>(max_parts | 1);  // odd: see hexkv_attend
+  dim3 grid(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (p->dtype) {
+    case HEXKV_BF16: rc = dispatch_d<__bf16>(p->head_dim, G, a, grid, kLaunchFt, s); break;
+    case HEXKV_F16: rc = dispatch_d<_Float16>(p->head_dim, G, a, grid, kLaunchFt, s); break;
+    default: rc = dispatch_d<float>(p->head_dim, G, a, grid, kLaunchFt, s); break;
+  }
+  if (rc != HEXKV_OK) return rc;
+  return check_launch("hexkv_ft_attend");
 }

@@ -409,3 +409,43 @@ extern "C" int hexkv_head_concat(const hexkv_block *src, int n_layers, int n_sha
   merge_layers(moves, n_layers);
   return run_moves(moves, static_cast<hipStream_t>(stream), what);
 }
+
+extern "C" int hexkv_ft_store(const void *kv, int64_t kv_batch_stride, int64_t kv_pos_stride, int64_t kv_stride,
+                              void *k_cache, void *v_cache, int batch, int seq_len, int64_t capacity,
+                              int kv_heads, int head_dim, int dtype, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_ft_store";
+  if (dtype != HEXKV_F16 && dtype != HEXKV_BF16 && dtype != HEXKV_F32)
+    return fail(HEXKV_EINVAL, "%s: unknown dtype %d", what, dtype);
+  const int64_t es = dtype == HEXKV_F32 ? 4 : 2, pack = 16 / es;
+  if (batch < 0 || seq_len < 0 || kv_heads < 1 || head_dim < 1 || capacity < 0)
+    return fail(HEXKV_EINVAL, "%s: negative or empty size", what);
+  if (head_dim % pack) return fail(HEXKV_EINVAL, "%s: head_dim %d not a multiple of %lld", what, head_dim,
+                                   static_cast<long long>(pack));
+  if (seq_len > capacity)
+    return fail(HEXKV_ERANGE, "%s: seq_len %d above capacity %lld", what, seq_len, static_cast<long long>(capacity));
+  if (kv_batch_stride < 0 || kv_pos_stride < 0 || kv_stride < 0)
+    return fail(HEXKV_EINVAL, "%s: negative stride", what);
+  if (batch == 0 || seq_len == 0) return HEXKV_OK;
+  if (!kv || !k_cache || !v_cache) return fail(HEXKV_EINVAL, "%s: null tensor", what);
+  const int64_t head = static_cast<int64_t>(head_dim) * es;  // bytes of one head row
+  const int64_t heads = static_cast<int64_t>(kv_heads) * head;
+  if (capacity > kMaxBytes / heads || batch > kMaxBytes / (capacity * heads))
+    return fail(HEXKV_ERANGE, "%s: caches larger than 64 TiB", what);
+  const char *src = static_cast<const char *>(kv);
+  // K: for every (head, 16-byte chunk) slice, seq_len positions of 16 bytes,
+  // from rows kv_pos_stride apart into chunk rows packed back to back.
+  Move k{src, static_cast<char *>(k_cache), 16, seq_len, heads / 16, kv_pos_stride * es, 16, 16, capacity * 16};
+  k.layers = batch;
+  k.src_layer = kv_batch_stride * es;
+  k.dst_layer = capacity * heads;
+  // V: per head, seq_len head rows into rows head bytes apart.
+  Move v{src + kv_stride * es, static_cast<char *>(v_cache), head, seq_len, kv_heads, kv_pos_stride * es, head,
+         head, capacity * head};
+  v.layers = batch;
+  v.src_layer = kv_batch_stride * es;
+  v.dst_layer = capacity * heads;
+  std::vector<Move> moves{k, v};
+  return run_moves(moves, static_cast<hipStream_t>(stream), what);
+}

@@ -17,10 +17,12 @@ class InferenceParams:
     """Per-request KV-cache state.
 
     ``key_value_memory_dict`` maps layer index -> cache tensor
-    ``[max_batch_size, max_sequence_len, 2, kv_heads, head_dim]``;
-    ``sequence_len_offset`` is the number of positions already cached (the
-    append position of the next token).  ``fused_ft_kernel`` must stay False:
-    the FasterTransformer cache layout is not part of this data path.
+    ``[max_batch_size, max_sequence_len, 2, kv_heads, head_dim]``, or with
+    ``fused_ft_kernel`` the FasterTransformer pair ``(K [B, H, D/pack, S,
+    pack], V [B, H, S, D])``; ``sequence_len_offset`` is the number of
+    positions already cached (the append position of the next token);
+    ``lengths_per_sample`` (int32, device), when set, gives each sequence's
+    own position on the FT path.
     """
     max_sequence_len: int
     max_batch_size: int = 1

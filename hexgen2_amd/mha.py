@@ -3,8 +3,11 @@
 * ``_update_kv_cache(kv, inference_params, layer_idx)`` -- append (and the
   prefill write) into the per-layer cache; hexgen/hexgen_core/modules/
   mha.py:255-288.
-* ``allocate_inference_cache(...)`` -- the non-FT cache of
-  ``MHA.allocate_inference_cache`` (mha.py:414-428).
+* ``allocate_inference_cache(...)`` -- ``MHA.allocate_inference_cache``
+  (mha.py:414-428): the ``[B, S, 2, H, D]`` cache, or with
+  ``fused_ft_kernel=True`` the FasterTransformer (FT) K/V pair.
+* ``_apply_rotary_single_query_attention(...)`` -- the FT decode step
+  (mha.py:310-337): rotary, append and attention over the FT caches.
 * ``FlashCrossAttention`` -- the attention module the reference's MHA calls at
   decode (mha.py:105-142); same constructor and ``forward`` signature.
 
@@ -22,9 +25,16 @@ from . import ops
 
 
 def allocate_inference_cache(batch_size: int, max_seqlen: int, num_heads_kv: int, head_dim: int,
-                             dtype: torch.dtype, device) -> torch.Tensor:
-    """``torch.empty(batch, max_seqlen, 2, kv_heads, head_dim)`` (mha.py:418-420)."""
-    return torch.empty(batch_size, max_seqlen, 2, num_heads_kv, head_dim, dtype=dtype, device=device)
+                             dtype: torch.dtype, device, fused_ft_kernel: bool = False):
+    """``torch.empty(batch, max_seqlen, 2, kv_heads, head_dim)`` (mha.py:418-420),
+    or with ``fused_ft_kernel`` the FT pair ``(K [batch, kv_heads, head_dim /
+    pack, max_seqlen, pack], V [batch, kv_heads, max_seqlen, head_dim])``,
+    pack = 4 for float32 and 8 for 16-bit data (mha.py:421-428)."""
+    if not fused_ft_kernel:
+        return torch.empty(batch_size, max_seqlen, 2, num_heads_kv, head_dim, dtype=dtype, device=device)
+    assert dtype in (torch.float16, torch.bfloat16, torch.float32)
+    k_shape, v_shape = ops.ft_cache_shapes(batch_size, num_heads_kv, max_seqlen, head_dim, dtype)
+    return (torch.empty(k_shape, dtype=dtype, device=device), torch.empty(v_shape, dtype=dtype, device=device))
 
 
 def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torch.Tensor:
@@ -33,7 +43,7 @@ def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torc
     ``layer_idx``'s cache (allocated on first use) and returns the view
     ``cache[batch_start:batch_end, :sequence_end]`` (mha.py:255-288)."""
     if inference_params.fused_ft_kernel:
-        raise NotImplementedError("the FasterTransformer cache layout is not supported")
+        return _update_ft_cache(kv, inference_params, layer_idx)
     num_heads, head_dim = kv.shape[-2:]
     cache = inference_params.key_value_memory_dict.get(layer_idx)
     if cache is None:
@@ -56,6 +66,67 @@ def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torc
         # uniform lengths into the cache shifted by sequence_start rows.
         ops.unpack_live([kv.reshape(-1)], [target[:, sequence_start:]], [kv.shape[1]] * kv.shape[0])
     return cache[batch_start:batch_end, :sequence_end]
+
+
+def _update_ft_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torch.Tensor:
+    """The FT branch of _update_kv_cache (mha.py:289-305), prefill only
+    (``sequence_len_offset == 0``): kv's positions ``[0, seqlen)`` go into the
+    layer's FT caches, allocated on first use.  (The reference first fills a
+    ``[B, S, 2, H, D]`` cache and converts all of it, mha.py:295-299; the
+    positions it writes are the same, the rest is uninitialised either way.)
+    Returns ``kv`` as the reference does."""
+    assert inference_params.sequence_len_offset == 0
+    assert kv.dtype in (torch.float16, torch.bfloat16, torch.float32)
+    num_heads, head_dim = kv.shape[-2:]
+    caches = inference_params.key_value_memory_dict.get(layer_idx)
+    if caches is None:
+        caches = allocate_inference_cache(inference_params.max_batch_size, inference_params.max_sequence_len,
+                                          num_heads, head_dim, kv.dtype, kv.device, fused_ft_kernel=True)
+        inference_params.key_value_memory_dict[layer_idx] = caches
+    k_cache, v_cache = caches
+    batch_start = inference_params.batch_size_offset
+    batch_end = batch_start + kv.shape[0]
+    assert batch_end <= v_cache.shape[0]
+    assert kv.shape[1] <= v_cache.shape[2]
+    ops.ft_store(kv, k_cache[batch_start:batch_end], v_cache[batch_start:batch_end])
+    return kv
+
+
+def _apply_rotary_single_query_attention(qkv: torch.Tensor, inference_params, layer_idx: int,
+                                         rotary_emb_dim: int, rotary_emb_base: float, kv=None,
+                                         rotary_emb_interleaved: bool = False) -> torch.Tensor:
+    """One FT decode step of layer ``layer_idx`` (mha.py:310-337).
+
+    qkv ``(B, 1, 3, H, D)`` when kv is None, else q ``(B, 1, H, D)`` with kv
+    ``(B, 1, 2, H_k, D)``.  The new token sits at ``lengths_per_sample[b]``
+    when the inference params carry per-sample lengths, else at
+    ``sequence_len_offset``; q and k are rotated there (``rotary_emb_dim``
+    leading dimensions, GPT-NeoX halves unless ``rotary_emb_interleaved``), k
+    and v are written to the FT caches and q attends to positions
+    ``[0, position]``.  Returns ``(B, 1, H, D)``."""
+    assert inference_params.fused_ft_kernel
+    if kv is None:
+        q, k, v = qkv[:, 0].unbind(dim=1)
+    else:
+        q = qkv[:, 0]
+        k, v = kv[:, 0].unbind(dim=1)
+    batch_start = inference_params.batch_size_offset
+    batch_end = batch_start + q.shape[0]
+    k_cache, v_cache = inference_params.key_value_memory_dict[layer_idx]
+    lengths = inference_params.lengths_per_sample
+    if lengths is not None:
+        positions = lengths[batch_start:batch_end].to(torch.int32).contiguous()
+        bias, max_position = 0, v_cache.shape[2] - 1
+    else:
+        positions, bias = None, inference_params.sequence_len_offset
+        max_position = bias
+    if k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    context = ops.ft_attend(q, k, v, k_cache[batch_start:batch_end], v_cache[batch_start:batch_end],
+                            max_position=max_position, positions=positions, position_bias=bias,
+                            rotary_dim=rotary_emb_dim, rotary_base=rotary_emb_base,
+                            rotary_neox=not rotary_emb_interleaved)
+    return context.unsqueeze(1)
 
 
 class FlashCrossAttention(nn.Module):

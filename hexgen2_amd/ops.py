@@ -288,6 +288,122 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     return out
 
 
+def ft_pack(dtype: torch.dtype) -> int:
+    """Elements per 16-byte K chunk of the FT layout: 4 for float32, 8 for
+    16-bit data (mha.py:423, generation.py:317)."""
+    return 4 if dtype == torch.float32 else 8
+
+
+def ft_cache_shapes(batch: int, kv_heads: int, capacity: int, head_dim: int, dtype: torch.dtype):
+    """(K shape, V shape) of one layer's FT cache:
+    ``[batch, kv_heads, head_dim // pack, capacity, pack]`` and
+    ``[batch, kv_heads, capacity, head_dim]`` (mha.py:420-427)."""
+    pack = ft_pack(dtype)
+    if head_dim % pack:
+        raise ValueError(f"head_dim {head_dim} is not a multiple of the FT pack size {pack}")
+    return (batch, kv_heads, head_dim // pack, capacity, pack), (batch, kv_heads, capacity, head_dim)
+
+
+def _check_ft_caches(k_cache: torch.Tensor, v_cache: torch.Tensor):
+    """(batch, kv_heads, capacity, head_dim) of a contiguous FT cache pair."""
+    if k_cache.dim() != 5 or v_cache.dim() != 4:
+        raise ValueError("FT caches are K [B, Hkv, D/pack, S, pack] and V [B, Hkv, S, D]")
+    batch, kv_heads, capacity, head_dim = v_cache.shape
+    if tuple(k_cache.shape) != ft_cache_shapes(batch, kv_heads, capacity, head_dim, v_cache.dtype)[0]:
+        raise ValueError(f"FT K cache {tuple(k_cache.shape)} does not match V cache {tuple(v_cache.shape)}")
+    if k_cache.dtype != v_cache.dtype or v_cache.dtype not in _DTYPES:
+        raise ValueError("FT caches must share one of float16, bfloat16, float32")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("FT caches must be contiguous (batch slices of them are)")
+    return batch, kv_heads, capacity, head_dim
+
+
+def ft_store(kv: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    """Write ``kv [B, s, 2, Hkv, D]`` into positions ``[0, s)`` of the FT
+    caches (one launch, a bit copy): the FT branch of _update_kv_cache,
+    mha.py:289-305."""
+    _require_device(kv, k_cache, v_cache)
+    batch, kv_heads, capacity, head_dim = _check_ft_caches(k_cache, v_cache)
+    if kv.dim() != 5 or kv.shape[2] != 2 or kv.shape[3] != kv_heads or kv.shape[4] != head_dim \
+            or kv.shape[0] != batch:
+        raise ValueError(f"kv {tuple(kv.shape)} does not fit FT caches of {batch} x {kv_heads} x {head_dim}")
+    if kv.dtype != v_cache.dtype or kv.device != v_cache.device:
+        raise ValueError("kv and the caches differ in dtype or device")
+    if kv.stride(4) != 1 or kv.stride(3) != head_dim:
+        kv = kv.contiguous()
+    rc = _lib.load().hexkv_ft_store(kv.data_ptr(), kv.stride(0), kv.stride(1), kv.stride(2),
+                                    k_cache.data_ptr(), v_cache.data_ptr(), batch, kv.shape[1], capacity,
+                                    kv_heads, head_dim, _DTYPES[kv.dtype], _stream(kv))
+    _lib.check(rc, "hexkv_ft_store")
+
+
+def _ft_params(q, k_new, v_new, k_cache, v_cache, out, positions, position_bias, max_position,
+               rotary_dim, rotary_base, rotary_neox, softmax_scale, partition) -> _lib.FtAttendParams:
+    batch, kv_heads, capacity, head_dim = _check_ft_caches(k_cache, v_cache)
+    if q.dim() != 3 or q.shape[0] != batch or q.shape[2] != head_dim or q.shape[1] % kv_heads:
+        raise ValueError(f"q {tuple(q.shape)} must be [batch, q_heads, head_dim] over FT caches of "
+                         f"{batch} x {kv_heads} x {head_dim}")
+    for name, t in (("k_new", k_new), ("v_new", v_new)):
+        if tuple(t.shape) != (batch, kv_heads, head_dim):
+            raise ValueError(f"{name} {tuple(t.shape)} must be [batch, kv_heads, head_dim]")
+    if k_new.stride() != v_new.stride():
+        raise ValueError("k_new and v_new must share strides")
+    for name, t in (("q", q), ("k_new", k_new), ("out", out)):
+        if t.dtype != v_cache.dtype:
+            raise ValueError(f"{name} dtype differs from the caches")
+        if t.stride(2) != 1 or t.stride(1) != head_dim:
+            raise ValueError(f"{name} heads must be contiguous [.., heads, head_dim]")
+    p = _lib.FtAttendParams()
+    p.dtype = _DTYPES[q.dtype]
+    p.batch, p.q_heads, p.kv_heads, p.head_dim = batch, q.shape[1], kv_heads, head_dim
+    p.softmax_scale = float(head_dim ** -0.5 if softmax_scale is None else softmax_scale)
+    p.q, p.q_batch_stride = q.data_ptr(), q.stride(0)
+    p.k_new, p.v_new, p.new_batch_stride = k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0)
+    p.k_cache, p.v_cache, p.capacity = k_cache.data_ptr(), v_cache.data_ptr(), capacity
+    p.out, p.out_batch_stride = out.data_ptr(), out.stride(0)
+    if positions is not None:
+        _require_device(positions)
+        if positions.dtype != torch.int32 or positions.numel() < batch or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int32 device tensor")
+        p.positions_dev = positions.data_ptr()
+    p.position_bias = int(position_bias)
+    p.max_position = int(max_position)
+    p.rotary_dim, p.rotary_base, p.rotary_neox = int(rotary_dim), float(rotary_base), 1 if rotary_neox else 0
+    p.partition = int(partition)
+    return p
+
+
+def ft_attend(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+              v_cache: torch.Tensor, *, max_position: int, positions: Optional[torch.Tensor] = None,
+              position_bias: int = 0, rotary_dim: int = 0, rotary_base: float = 10000.0,
+              rotary_neox: bool = True, softmax_scale: Optional[float] = None,
+              out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+              partition: int = 0) -> torch.Tensor:
+    """One decode step over FT caches (one launch plus the split merge):
+    rotate ``q [B, Hq, D]`` and ``k_new [B, Hkv, D]`` at position
+    ``pos_b = positions[b] + position_bias`` (``position_bias`` alone when
+    ``positions`` is None), write ``k_new``/``v_new`` at ``pos_b``, attend over
+    ``[0, pos_b]``.  The semantics of ft_attention.single_query_attention as
+    mha.py:310-337 calls it; ``max_position`` is a host bound on every
+    ``pos_b`` (below the cache capacity)."""
+    _require_device(q, k_new, v_new, k_cache, v_cache)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    p = _ft_params(q, k_new, v_new, k_cache, v_cache, out, positions, position_bias, max_position,
+                   rotary_dim, rotary_base, rotary_neox, softmax_scale, partition)
+    lib = _lib.load()
+    need = int(lib.hexkv_ft_attend_workspace_bytes(ctypes.byref(p)))
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        _require_device(workspace)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    rc = lib.hexkv_ft_attend(ctypes.byref(p), ws_ptr, ws_bytes, _stream(q))
+    _lib.check(rc, "hexkv_ft_attend")
+    return out
+
+
 class AttendPlan:
     """Prebuilt ``hexkv_attend`` parameters for a decode loop on one geometry.
 

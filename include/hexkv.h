@@ -202,6 +202,82 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
                  size_t workspace_bytes, hexkv_stream_t stream);
 
 /*
+ * The FasterTransformer ("FT") cache layout of hexgen_core's fused decode
+ * path (fused_ft_kernel=True; the layout the reference's CUDA-graph decode
+ * uses): per layer
+ *   K  [batch][kv_heads][head_dim / pack][capacity][pack]
+ *   V  [batch][kv_heads][capacity][head_dim]
+ * with pack = 8 for 16-bit data and 4 for float32, so one K position of one
+ * head is head_dim / pack chunks of 16 bytes, capacity * 16 bytes apart.
+ */
+
+/*
+ * Writes positions [0, seq_len) of kv ([batch][.. seq_len ..][2][kv_heads]
+ * [head_dim], heads and head_dim contiguous; strides in elements, kv_stride
+ * from K to V) into the FT caches, positions [0, seq_len) of each sequence.
+ * A bit copy.
+ *
+ * Replaces the FT branch of _update_kv_cache
+ * (hexgen/hexgen_core/modules/mha.py:289-305): the conversion of a filled
+ * [B, S, 2, H, D] cache into the FT pair (rearranges at mha.py:296-298) and
+ * the direct prefill write into FT caches (mha.py:301-305).
+ */
+int hexkv_ft_store(const void *kv, int64_t kv_batch_stride, int64_t kv_pos_stride, int64_t kv_stride,
+                   void *k_cache, void *v_cache, int batch, int seq_len, int64_t capacity,
+                   int kv_heads, int head_dim, int dtype, hexkv_stream_t stream);
+
+/* One decode step over FT caches: rotary on q and on the new K, append of
+ * the new K/V at each sequence's position, single-query GQA attention over
+ * positions [0, position]. */
+typedef struct hexkv_ft_attend_params {
+  int dtype;       /* enum hexkv_dtype, shared by every tensor            */
+  int batch;
+  int q_heads;
+  int kv_heads;    /* divides q_heads                                      */
+  int head_dim;    /* 16, 32, 64, 128 or 256                               */
+  float softmax_scale;
+  const void *q;   /* [batch][q_heads][head_dim], heads contiguous         */
+  int64_t q_batch_stride;
+  const void *k_new, *v_new; /* [batch][kv_heads][head_dim] each          */
+  int64_t new_batch_stride;
+  void *k_cache, *v_cache;   /* FT layouts above                           */
+  int64_t capacity;
+  void *out;       /* [batch][q_heads][head_dim]                           */
+  int64_t out_batch_stride;
+  /* Position of sequence b's new token: pos_b = (positions_dev ?
+   * positions_dev[b] : 0) + position_bias; max_position bounds every pos_b
+   * and must be below capacity. */
+  const int32_t *positions_dev;
+  int32_t position_bias;
+  int32_t max_position;
+  /* Rotary embedding of q and the new K at pos_b: the first rotary_dim
+   * dimensions of each head turn in pairs, pair j by pos_b *
+   * rotary_base^(-2j / rotary_dim) radians; pairs (j, j + rotary_dim/2) when
+   * rotary_neox, else (2j, 2j + 1).  rotary_dim 0: no rotation. */
+  int rotary_dim;
+  float rotary_base;
+  int rotary_neox;
+  int partition;   /* as in hexkv_attend_params */
+} hexkv_ft_attend_params;
+
+/* Workspace bytes hexkv_ft_attend needs (same role as for hexkv_attend). */
+size_t hexkv_ft_attend_workspace_bytes(const hexkv_ft_attend_params *p);
+
+/*
+ * Replaces the fused decode attention of the FT path,
+ *   _apply_rotary_single_query_attention
+ *   (hexgen/hexgen_core/modules/mha.py:310-337), which calls
+ *   ft_attention.single_query_attention (FasterTransformer's masked
+ *   multi-head attention, an extension the reference does not vendor) with
+ *   lengths_per_sample or sequence_len_offset as the position
+ *   (mha.py:325-335).  q and the new K are rotated and rounded to the data
+ *   type, the new K/V are written at pos_b, and
+ *   out[b,h] = sum_{s <= pos_b} softmax_s(q.K[b,s,h/g] * scale) V[b,s,h/g].
+ */
+int hexkv_ft_attend(const hexkv_ft_attend_params *p, void *workspace, size_t workspace_bytes,
+                    hexkv_stream_t stream);
+
+/*
  * Legacy KV formats of HexGen's earlier disaggregation scripts
  * (hexgen/llama/): the flat-concatenated packet, zero-padded request
  * batching and the tensor-parallel head concatenation.  Each is a strided

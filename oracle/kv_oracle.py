@@ -23,6 +23,19 @@ Functions and the reference code each one restates:
                                          21-26 / 50-57 (flat KV packet)
 * ``batch_pad`` hexgen/llama/kv_cache_batch.py:11-22 (zero-pad + stack)
 * ``concat_dim`` hexgen/llama/tensor_parallel_dim_concat.py:9-19 (TP heads)
+* ``ft_layout`` / ``ft_unlayout``  hexgen/hexgen_core/modules/mha.py:296-298,
+                                         301-305 (the FasterTransformer K/V
+                                         layouts, rearrange patterns) and its
+                                         inverse
+* ``round_to``  rounding to float16 / bfloat16 / float32, nearest-even
+* ``rotary``    the rotary embedding applied to q and k at the token's
+                                         position on the FT path (mha.py:
+                                         310-337 -> ft_attention, not vendored;
+                                         GPT-NeoX halves or GPT-J pairs,
+                                         angle pos * base^(-2j / rot_dim))
+* ``ft_decode`` mha.py:310-337: rotate q and k (rounded to the data type),
+                                         write k, v at each sequence's
+                                         position, attend over [0, position]
 
 Pinning (tests/test_oracle.py): pack/unpack/append against element-by-element
 Python loops on small inputs, the round-trip and untouched-row invariants, and
@@ -33,7 +46,14 @@ scalar-loop restatement on small shapes, and torch's
 scaled_dot_product_attention in float64.  The legacy formats against the
 library routines the reference calls (torch.cat, torch.nn.functional.pad with
 the reference's pad tuple) and against their inverses (slicing a batch or a
-concatenation back into its parts recovers them; padding is zero).
+concatenation back into its parts recovers them; padding is zero).  The FT
+layouts against einops.rearrange with the reference's own patterns and
+against their inverse; ``rotary`` against closed forms (position 0 and
+rot_dim 0 are the identity, every pair keeps its norm, a 2-vector turns by
+pos radians) and, for the GPT-NeoX form, against transformers' Llama
+``apply_rotary_pos_emb``, with the GPT-J form tied to it by the pair
+permutation; ``round_to`` against torch's casts; ``ft_decode`` without
+rotation against ``append`` + ``attend``.
 """
 from __future__ import annotations
 
@@ -214,3 +234,76 @@ def concat_dim(shards: Sequence[np.ndarray], dim: int = 3) -> np.ndarray:
     `dim`, the KV-head dimension of [B, S, 2, H, D] by default
     (tensor_parallel_dim_concat.py:9-19)."""
     return np.concatenate(list(shards), axis=dim)
+
+
+# ------------------------------------------------------ FasterTransformer ---
+
+
+def ft_layout(cache: np.ndarray, pack: int):
+    """[B, S, 2, H, D] -> (K [B, H, D/pack, S, pack], V [B, H, S, D]): the
+    rearranges 'b s h (d packsize) -> b h d s packsize' and
+    'b s h d -> b h s d' of mha.py:296-298."""
+    b, s, _, h, d = cache.shape
+    k = cache[:, :, 0].reshape(b, s, h, d // pack, pack).transpose(0, 2, 3, 1, 4)
+    v = cache[:, :, 1].transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(k), np.ascontiguousarray(v)
+
+
+def ft_unlayout(k: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """Inverse of ``ft_layout``: the FT pair back to [B, S, 2, H, D]."""
+    b, h, dp, s, p = k.shape
+    kk = k.transpose(0, 3, 1, 2, 4).reshape(b, s, h, dp * p)
+    vv = v.transpose(0, 2, 1, 3)
+    return np.stack([kk, vv], axis=2)
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """x rounded to ``dtype`` ("float16", "bfloat16", "float32"), nearest
+    even, returned as float64."""
+    x32 = np.asarray(x, dtype=np.float64).astype(np.float32)
+    if dtype == "float32":
+        return x32.astype(np.float64)
+    if dtype == "float16":
+        return x32.astype(np.float16).astype(np.float64)
+    if dtype == "bfloat16":
+        bits = x32.view(np.uint32).astype(np.uint64)
+        bits = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000
+        return bits.astype(np.uint32).view(np.float32).astype(np.float64)
+    raise ValueError(dtype)
+
+
+def rotary(x: np.ndarray, pos: int, rot_dim: int, base: float, neox: bool) -> np.ndarray:
+    """Rotary embedding of x [..., D] at position ``pos`` (float64): pair j of
+    the first rot_dim dimensions -- (j, j + rot_dim/2) in the GPT-NeoX form,
+    (2j, 2j + 1) in the GPT-J form -- turns by pos * base^(-2j / rot_dim)."""
+    out = np.array(x, dtype=np.float64)
+    half = rot_dim // 2
+    for j in range(half):
+        theta = pos * base ** (-2.0 * j / rot_dim)
+        c, s = math.cos(theta), math.sin(theta)
+        i0, i1 = (j, j + half) if neox else (2 * j, 2 * j + 1)
+        x0, x1 = out[..., i0].copy(), out[..., i1].copy()
+        out[..., i0] = x0 * c - x1 * s
+        out[..., i1] = x0 * s + x1 * c
+    return out
+
+
+def ft_decode(q, k_new, v_new, k_ft, v_ft, positions, rot_dim=0, base=10000.0, neox=True,
+              dtype="float32", softmax_scale=None):
+    """One FT decode step (mha.py:310-337): q [B, Hq, D], k_new/v_new
+    [B, Hkv, D], FT caches; sequence b's token sits at positions[b].  q and
+    k are rotated there and rounded to ``dtype``; k and v are written at that
+    position; q attends to [0, position].  Returns (out [B, Hq, D] float64,
+    K', V') with the caches' dtype preserved."""
+    pack = k_ft.shape[-1]
+    cache = ft_unlayout(np.asarray(k_ft), np.asarray(v_ft)).astype(np.float64)
+    batch = q.shape[0]
+    qr = np.stack([round_to(rotary(q[b], positions[b], rot_dim, base, neox), dtype) for b in range(batch)])
+    kr = np.stack([round_to(rotary(k_new[b], positions[b], rot_dim, base, neox), dtype)
+                   for b in range(batch)])
+    for b in range(batch):
+        cache[b, positions[b], 0] = kr[b]
+        cache[b, positions[b], 1] = np.asarray(v_new[b], dtype=np.float64)
+    out = attend(qr[:, None], cache, [p + 1 for p in positions], softmax_scale=softmax_scale)[:, 0]
+    k2, v2 = ft_layout(cache, pack)
+    return out, k2.astype(np.asarray(k_ft).dtype), v2.astype(np.asarray(v_ft).dtype)

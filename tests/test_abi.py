@@ -34,6 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 
 @pytest.mark.parametrize("c_name,mirror", [("hexkv_attend_params", _lib.AttendParams),
+                                            ("hexkv_ft_attend_params", _lib.FtAttendParams),
                                             ("hexkv_block", _lib.Block),
                                             ("hexkv_ipc_handle", _lib.IpcHandle)])
 def test_struct_layouts_match_c(tmp_path, c_name, mirror):
@@ -101,6 +102,26 @@ def test_legacy_format_validation_fails_before_launch():
     assert lib.hexkv_head_concat(shards, 1, 2, ptr, None) == _lib.HEXKV_EINVAL
     shards[1].height, shards[1].width = 6, 512
     assert lib.hexkv_head_concat(shards, 2, 1, ptr, None) == _lib.HEXKV_EINVAL
+
+
+def test_ft_validation_fails_before_launch():
+    lib = _lib.load()
+    P = _lib.FtAttendParams
+    base = dict(dtype=1, batch=1, q_heads=4, kv_heads=2, head_dim=64, softmax_scale=0.125, capacity=8,
+                max_position=3, q=16, k_new=16, v_new=16, k_cache=16, v_cache=16, out=16)
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "max_position": 8})), None, 0, None) == _lib.HEXKV_ERANGE
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "rotary_dim": 3})), None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "rotary_dim": 66})), None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "rotary_dim": 64})), None, 0, None) == _lib.HEXKV_EINVAL
+    assert b"rotary_base" in lib.hexkv_last_error()
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "head_dim": 48})), None, 0, None) == _lib.HEXKV_EUNSUPPORTED
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "q_heads": 3})), None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "out": 0})), None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_ft_attend(ctypes.byref(P(**{**base, "batch": 0})), None, 0, None) == _lib.HEXKV_OK
+    # ft_store: more positions than capacity; a head_dim that is not whole 16-byte chunks
+    assert lib.hexkv_ft_store(16, 0, 0, 0, 16, 16, 1, 9, 8, 2, 64, 1, None) == _lib.HEXKV_ERANGE
+    assert lib.hexkv_ft_store(16, 0, 0, 0, 16, 16, 1, 4, 8, 2, 12, 1, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_ft_store(None, 0, 0, 0, 16, 16, 1, 0, 8, 2, 64, 1, None) == _lib.HEXKV_OK
 
 
 def test_status_codes_map_to_reference_exception_types():

@@ -264,3 +264,82 @@ def test_concat_dim_default_is_the_kv_head_dim():
     assert got.shape == (2, 3, 2, 8, 4)
     for h in range(8):
         np.testing.assert_array_equal(got[:, :, :, h], shards[h // 2][:, :, :, h % 2])
+
+
+# ------------------------------------------------------ FasterTransformer ---
+
+
+@pytest.mark.parametrize("dtype,pack", [(np.float16, 8), (np.float32, 4)])
+def test_ft_layout_is_the_reference_rearrange(dtype, pack):
+    """ft_layout == einops.rearrange with the patterns of mha.py:296-298."""
+    import einops
+    rng = np.random.default_rng(3)
+    cache = rng.standard_normal((2, 7, 2, 3, 16)).astype(dtype)
+    k, v = oracle.ft_layout(cache, pack)
+    t = torch.from_numpy(cache)
+    k_ref = einops.rearrange(t[:, :, 0], "b s h (d packsize) -> b h d s packsize", packsize=pack).contiguous()
+    v_ref = einops.rearrange(t[:, :, 1], "b s h d -> b h s d").contiguous()
+    assert k.shape == (2, 3, 16 // pack, 7, pack) and v.shape == (2, 3, 7, 16)
+    np.testing.assert_array_equal(k, k_ref.numpy())
+    np.testing.assert_array_equal(v, v_ref.numpy())
+    np.testing.assert_array_equal(oracle.ft_unlayout(k, v), cache)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+def test_round_to_matches_torch_casts(dtype):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(4096) * 10.0 ** rng.integers(-3, 4, 4096)
+    got = oracle.round_to(x, dtype)
+    want = torch.from_numpy(x.astype(np.float32)).to(getattr(torch, dtype)).to(torch.float64).numpy()
+    np.testing.assert_array_equal(got, want)
+
+
+def test_rotary_closed_forms():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 16))
+    for neox in (True, False):
+        np.testing.assert_array_equal(oracle.rotary(x, 0, 16, 10000.0, neox), x)  # position 0
+        np.testing.assert_array_equal(oracle.rotary(x, 9, 0, 10000.0, neox), x)   # no rotary dims
+        y = oracle.rotary(x, 37, 8, 500.0, neox)
+        np.testing.assert_array_equal(y[:, 8:], x[:, 8:])                         # beyond rot_dim
+        pairs = [(j, j + 4) if neox else (2 * j, 2 * j + 1) for j in range(4)]
+        for i0, i1 in pairs:                                                      # each pair keeps its norm
+            np.testing.assert_allclose(np.hypot(y[:, i0], y[:, i1]), np.hypot(x[:, i0], x[:, i1]), rtol=1e-12)
+    # a 2-vector turns by pos radians (pair 0 has frequency 1)
+    v = np.array([1.0, 0.0])
+    np.testing.assert_allclose(oracle.rotary(v, 3, 2, 10000.0, True), [math.cos(3), math.sin(3)], atol=1e-15)
+
+
+@pytest.mark.parametrize("pos,rot_dim,base", [(1, 64, 10000.0), (1234, 64, 10000.0), (77, 32, 500000.0)])
+def test_rotary_neox_matches_transformers_llama(pos, rot_dim, base):
+    """The GPT-NeoX form equals transformers' Llama apply_rotary_pos_emb
+    (rotate_half) on the rotated dimensions; the GPT-J form equals it after
+    gathering each (2j, 2j+1) pair into (j, j + rot_dim/2)."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    rng = np.random.default_rng(pos)
+    q = rng.standard_normal((1, 2, 1, rot_dim))
+    inv_freq = 1.0 / (base ** (torch.arange(0, rot_dim, 2, dtype=torch.float64) / rot_dim))
+    freqs = pos * inv_freq
+    emb = torch.cat((freqs, freqs))[None, None]
+    qt = torch.from_numpy(q)
+    q_hf, _ = apply_rotary_pos_emb(qt, qt, emb.cos(), emb.sin())
+    np.testing.assert_allclose(oracle.rotary(q, pos, rot_dim, base, True), q_hf.numpy(), rtol=1e-12, atol=1e-12)
+    perm = np.concatenate([np.arange(0, rot_dim, 2), np.arange(1, rot_dim, 2)])  # pairs -> halves
+    gptj = oracle.rotary(q, pos, rot_dim, base, False)
+    np.testing.assert_allclose(gptj[..., perm], oracle.rotary(q[..., perm], pos, rot_dim, base, True),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_ft_decode_without_rotary_is_append_then_attend():
+    rng = np.random.default_rng(6)
+    batch, cap, hkv, hq, d = 3, 12, 2, 4, 8
+    cache = rng.standard_normal((batch, cap, 2, hkv, d)).astype(np.float32)
+    q = rng.standard_normal((batch, hq, d)).astype(np.float32)
+    kv_new = rng.standard_normal((batch, 2, hkv, d)).astype(np.float32)
+    positions = [0, 5, 11]
+    k_ft, v_ft = oracle.ft_layout(cache, 4)
+    out, k2, v2 = oracle.ft_decode(q, kv_new[:, 0], kv_new[:, 1], k_ft, v_ft, positions)
+    appended = oracle.append(cache, kv_new, positions)
+    want = oracle.attend(q[:, None], appended, [p + 1 for p in positions])[:, 0]
+    np.testing.assert_allclose(out, want, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(oracle.ft_unlayout(k2, v2), appended)

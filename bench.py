@@ -217,6 +217,62 @@ def measure_formats(device, reps=5):
     return out
 
 
+def measure_ft(device, steps=16):
+    """Secondary figures for the FasterTransformer-layout path on one
+    Llama-3-8B-shaped layer, outside the timed steps: hexkv_ft_store of a
+    64 x 4096-position prefill (GB/s of bytes read + written) and
+    ``steps`` hexkv_ft_attend decode steps with full-width rotary over the
+    workload's ragged lengths (µs per call; GB/s with the byte accounting of
+    hexkv_attend)."""
+    w = workload("llama3-8b")
+    B, H, Hq, D, dtype = w.batch, w.kv_heads, w.q_heads, w.head_dim, w.dtype
+    g = torch.Generator(device=device).manual_seed(w.seed + 7)
+    k_shape, v_shape = ops.ft_cache_shapes(B, H, w.capacity, D, dtype)
+    k_cache = torch.empty(k_shape, dtype=dtype, device=device).normal_(generator=g)
+    v_cache = torch.empty(v_shape, dtype=dtype, device=device).normal_(generator=g)
+    out = {}
+    kv = torch.randn((B, 4096, 2, H, D), generator=g, device=device).to(dtype)
+    ops.ft_store(kv, k_cache, v_cache)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(5):
+        ops.ft_store(kv, k_cache, v_cache)
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / 5
+    nbytes = 2 * kv.numel() * kv.element_size()
+    out["ft_store"] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "ms": round(ms, 4), "bytes": nbytes,
+                       "shape": list(kv.shape)}
+    del kv
+    q = torch.randn((B, Hq, D), generator=g, device=device).to(dtype)
+    new = torch.randn((B, 2, H, D), generator=g, device=device).to(dtype)
+    lens = torch.tensor(w.lens, dtype=torch.int32, device=device)
+    max_len = max(w.lens)
+    ws = torch.empty(max(ops.ft_attend_workspace_bytes(q, k_cache, v_cache, max_len + steps), 16),
+                     dtype=torch.uint8, device=device)
+    res = torch.empty_like(q)
+
+    def step(t):
+        ops.ft_attend(q, new[:, 0], new[:, 1], k_cache, v_cache, max_position=max_len + t, positions=lens,
+                      position_bias=t, rotary_dim=D, out=res, workspace=ws)
+    step(0)
+    torch.cuda.synchronize()
+    ev[0].record()
+    for t in range(steps):
+        step(t)
+    ev[1].record()
+    torch.cuda.synchronize()
+    us = ev[0].elapsed_time(ev[1]) * 1e3 / steps
+    nbytes = sum(w.attend_bytes(t) for t in range(steps)) / steps
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out["ft_attend"] = {"us_per_layer": round(us, 1), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "rotary_dim": D, "steps": steps}
+    del k_cache, v_cache
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(w, job, budget_s):
     """The reference's PyTorch ops (oracle/cpu_path.py) on host cores, on a
     bounded sample: 2 layers of pack+unpack and 1 layer x a few decode steps
@@ -391,6 +447,8 @@ def main():
         torch.cuda.empty_cache()
         result["formats"] = measure_formats(device)
         log(f"legacy formats {result['formats']}")
+        result["ft_layout"] = measure_ft(device)
+        log(f"FT layout {result['ft_layout']}")
     print(json.dumps(result), flush=True)
 
 

@@ -373,6 +373,15 @@ def _ft_params(q, k_new, v_new, k_cache, v_cache, out, positions, position_bias,
     return p
 
 
+def ft_attend_workspace_bytes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              max_position: int, partition: int = 0) -> int:
+    """Workspace bytes ``ft_attend`` needs for this geometry and bound."""
+    batch, kv_heads, _, head_dim = _check_ft_caches(k_cache, v_cache)
+    new = q.new_empty((batch, kv_heads, head_dim))
+    p = _ft_params(q, new, new, k_cache, v_cache, q, None, 0, max_position, 0, 10000.0, True, None, partition)
+    return int(_lib.load().hexkv_ft_attend_workspace_bytes(ctypes.byref(p)))
+
+
 def ft_attend(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
               v_cache: torch.Tensor, *, max_position: int, positions: Optional[torch.Tensor] = None,
               position_bias: int = 0, rotary_dim: int = 0, rotary_base: float = 10000.0,

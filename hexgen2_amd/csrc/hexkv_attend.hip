@@ -289,6 +289,10 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   __shared__ float s_acc[kAttWaves][G][D];
   __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
   __shared__ float s_kn[FT ? D : 1];
+  // FT: two staged K tiles, STEP positions of D / VEC 16-byte chunks each,
+  // one padded row per position.
+  constexpr int KT_PITCH = D / VEC * 16 + 16;
+  __shared__ __attribute__((aligned(16))) char s_kt[FT ? 2 * STEP * KT_PITCH : 16];
   Work w;
   if (!begin_work<T, D, G>(a, w)) return;
 
@@ -420,7 +424,83 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   // i + 1 are in flight while iteration i computes.  Then the tail.
   const int n_full = w.n_cache / STEP * STEP;
   int i0 = 0;
-  if constexpr (PF) {
+  if constexpr (FT) {
+    // K of the FT layout is staged through LDS: the workgroup loads a tile of
+    // STEP positions plane by plane (consecutive threads, consecutive
+    // positions: STEP x 16-byte runs), stores it position-major, and every
+    // lane group then reads its position's chunks as in the standard layout.
+    // Double-buffered: tile t + 1's loads are in flight while tile t
+    // computes, one barrier per tile.  V is read directly, as before.
+    constexpr int CH = D / VEC, CPT = STEP * CH / kAttThreads;
+    static_assert(STEP * CH % kAttThreads == 0, "K tile does not split over the workgroup");
+    auto kt_fetch = [&](int t0, u32x4 (&kt)[CPT]) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int q = tid + c * kAttThreads, r = q % STEP, j = q / STEP;
+        const int p = min(t0 + r, w.n_cache - 1);
+        kt[c] = load16(kseq, static_cast<uint32_t>(w.p0 + p) * 16u + static_cast<uint32_t>(j) * kchunk);
+      }
+    };
+    auto kt_store = [&](int buf, const u32x4 (&kt)[CPT]) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) {
+        const int q = tid + c * kAttThreads, r = q % STEP, j = q / STEP;
+        *reinterpret_cast<u32x4 *>(s_kt + (buf * STEP + r) * KT_PITCH + j * 16) = kt[c];
+      }
+    };
+    auto v_fetch = [&](int t0, Slots &vr) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int p = min(t0 + u * NG + gid, w.n_cache - 1);
+        const uint32_t voff = static_cast<uint32_t>(w.p0 + p) * vrow_bytes + lane_off;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) vr[u][v] = load16(vseq, voff + v * 16);
+      }
+    };
+    auto k_read = [&](int buf, Slots &kr) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+          kr[u][v] = *reinterpret_cast<const u32x4 *>(s_kt + (buf * STEP + u * NG + gid) * KT_PITCH +
+                                                      (sub * NV + v) * 16);
+    };
+    const int nfull = w.n_cache / STEP, ntiles = (w.n_cache + STEP - 1) / STEP;
+    if (ntiles > 0) {
+      u32x4 kt[CPT];
+      Slots vr;
+      kt_fetch(0, kt);
+      v_fetch(0, vr);
+      kt_store(0, kt);
+      __syncthreads();
+      for (int t = 0; t < nfull; ++t) {
+        const int t0 = t * STEP;
+        const bool more = t + 1 < ntiles;
+        Slots vnext;
+        if (more) {
+          kt_fetch(t0 + STEP, kt);
+          v_fetch(t0 + STEP, vnext);
+        }
+        Slots kr;
+        k_read(t & 1, kr);
+        consume(t0, kr, vr, std::false_type{});
+        if (more) {
+          kt_store((t + 1) & 1, kt);
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < NV; ++v) vr[u][v] = vnext[u][v];
+        }
+        __syncthreads();
+      }
+      if (nfull < ntiles) {  // the partial last tile, loaded and staged above
+        Slots kr;
+        k_read(nfull & 1, kr);
+        consume(nfull * STEP, kr, vr, std::true_type{});
+      }
+    }
+    i0 = w.n_cache;
+  } else if constexpr (PF) {
     if (n_full > 0) {
       Slots ka, va;
       fetch(0, ka, va, std::false_type{});

@@ -1,7 +1,8 @@
 // Single-query GQA decode attention over the KV cache, with optional fused
 // append of the new token's K/V (hexkv_attend in hexkv.h), and the same over
 // the FasterTransformer cache layouts with rotary embedding (hexkv_ft_attend:
-// the VALU kernel with FT addressing and a rotary prologue).
+// the VALU kernel with a rotary prologue, K tiles staged through LDS to turn
+// the FT chunk planes back into position-major rows, V read directly).
 //
 // Work decomposition (split-K, "flash-decoding"):
 //   grid = (partition, q-head group, query row).  A workgroup (4 waves) owns

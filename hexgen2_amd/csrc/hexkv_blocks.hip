@@ -114,6 +114,51 @@ __global__ __launch_bounds__(kSpanThreads) void span_copy_kernel(const SpanArgs 
   }
 }
 
+// FT store (hexkv_ft_store): kv rows [2][H][D] -> K chunk planes and
+// head-major V.  A workgroup takes up to kFtRows positions x kFtCols 16-byte
+// chunks of one sequence: it reads the K chunks row by row (whole-row runs)
+// into LDS and writes them out plane by plane (kFtRows x 16-byte runs); the V
+// chunks go straight from the rows to their head rows (head_dim x element runs).
+constexpr int kFtRows = 16, kFtCols = 128;
+
+struct FtStoreArgs {
+  const char *src;  // K of sequence 0, position 0
+  int64_t src_batch, src_pos, src_kv;
+  char *k, *v;
+  int64_t k_batch, v_batch, k_plane, v_head;  // bytes
+  int32_t head_chunks;                        // 16-byte chunks per head row
+  int32_t chunks;                             // 16-byte chunks of a row's K (= of its V)
+  int32_t seq_len;
+};
+
+__global__ __launch_bounds__(kSpanThreads) void ft_store_kernel(const FtStoreArgs a) {
+  __shared__ u32x4 s_tile[kFtRows][kFtCols + 1];  // padded: plane-wise reads spread over the banks
+  const int tid = threadIdx.x;
+  const int p0 = blockIdx.x * kFtRows, c0 = blockIdx.y * kFtCols;
+  const int64_t b = blockIdx.z;
+  const int np = min(kFtRows, a.seq_len - p0), nc = min(kFtCols, a.chunks - c0);
+  const char *rows = a.src + b * a.src_batch + static_cast<int64_t>(p0) * a.src_pos;
+  for (int q = tid; q < kFtRows * kFtCols; q += kSpanThreads) {
+    const int p = q / kFtCols, c = q % kFtCols;
+    if (p < np && c < nc) {
+      const char *row = rows + p * a.src_pos + static_cast<int64_t>(c0 + c) * 16;
+      s_tile[p][c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row));
+      const int g = c0 + c, h = g / a.head_chunks, cc = g - h * a.head_chunks;
+      char *dst = a.v + b * a.v_batch + h * a.v_head + (static_cast<int64_t>(p0 + p) * a.head_chunks + cc) * 16;
+      __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + a.src_kv)),
+                                  reinterpret_cast<u32x4 *>(dst));
+    }
+  }
+  __syncthreads();
+  for (int q = tid; q < kFtRows * kFtCols; q += kSpanThreads) {
+    const int c = q / kFtRows, p = q % kFtRows;
+    if (p < np && c < nc) {
+      char *dst = a.k + b * a.k_batch + (c0 + c) * a.k_plane + static_cast<int64_t>(p0 + p) * 16;
+      __builtin_nontemporal_store(s_tile[p][c], reinterpret_cast<u32x4 *>(dst));
+    }
+  }
+}
+
 // ------------------------------------------------------------------ host ---
 
 // One span before tiling (all sizes in bytes): `layers` copies of a
@@ -434,6 +479,28 @@ extern "C" int hexkv_ft_store(const void *kv, int64_t kv_batch_stride, int64_t k
   if (capacity > kMaxBytes / heads || batch > kMaxBytes / (capacity * heads))
     return fail(HEXKV_ERANGE, "%s: caches larger than 64 TiB", what);
   const char *src = static_cast<const char *>(kv);
+  if (aligned16(kv) && aligned16(k_cache) && aligned16(v_cache) && (kv_batch_stride * es) % 16 == 0 &&
+      (kv_pos_stride * es) % 16 == 0 && (kv_stride * es) % 16 == 0 && head % 16 == 0 && heads / 16 <= INT32_MAX &&
+      batch <= 65535) {
+    FtStoreArgs a;
+    a.src = src;
+    a.src_batch = kv_batch_stride * es;
+    a.src_pos = kv_pos_stride * es;
+    a.src_kv = kv_stride * es;
+    a.k = static_cast<char *>(k_cache);
+    a.v = static_cast<char *>(v_cache);
+    a.k_batch = a.v_batch = capacity * heads;
+    a.k_plane = capacity * 16;
+    a.v_head = capacity * head;
+    a.head_chunks = static_cast<int32_t>(head / 16);
+    a.chunks = static_cast<int32_t>(heads / 16);
+    a.seq_len = seq_len;
+    const dim3 grid((seq_len + kFtRows - 1) / kFtRows, (a.chunks + kFtCols - 1) / kFtCols, batch);
+    if (grid.y > 65535) return fail(HEXKV_ERANGE, "%s: rows of more than %d chunks", what, 65535 * kFtCols);
+    ft_store_kernel<<<grid, kSpanThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+    return check_launch(what);
+  }
+  // Unaligned views: the span engine.
   // K: for every (head, 16-byte chunk) slice, seq_len positions of 16 bytes,
   // from rows kv_pos_stride apart into chunk rows packed back to back.
   Move k{src, static_cast<char *>(k_cache), 16, seq_len, heads / 16, kv_pos_stride * es, 16, 16, capacity * 16};

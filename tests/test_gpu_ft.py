@@ -85,6 +85,24 @@ def test_ft_store_from_a_cache_view_into_a_batch_slice(device):
     assert (bits(v_cache)[[0, 3]] == 0).all() and (bits(v_cache)[1:3, :, 17:] == 0).all()
 
 
+def test_ft_store_from_an_unaligned_view(device):
+    """A source that is not 16-byte aligned takes the span-engine path."""
+    dtype, batch, seq, cap, hkv, d = torch.float16, 2, 33, 40, 2, 64
+    g = torch.Generator(device=device).manual_seed(13)
+    flat = torch.randn(batch * seq * 2 * hkv * d + 1, generator=g, device=device).to(dtype)
+    kv = flat[1:].view(batch, seq, 2, hkv, d)
+    assert kv.data_ptr() % 16
+    k_shape, v_shape = ops.ft_cache_shapes(batch, hkv, cap, d, dtype)
+    k_cache = torch.zeros(k_shape, dtype=dtype, device=device)
+    v_cache = torch.zeros(v_shape, dtype=dtype, device=device)
+    ops.ft_store(kv, k_cache, v_cache)
+    torch.cuda.synchronize()
+    k_ref, v_ref = oracle.ft_layout(bits(kv), ops.ft_pack(dtype))
+    np.testing.assert_array_equal(bits(k_cache)[:, :, :, :seq], k_ref)
+    np.testing.assert_array_equal(bits(v_cache)[:, :, :seq], v_ref)
+    assert (bits(k_cache)[:, :, :, seq:] == 0).all() and (bits(v_cache)[:, :, seq:] == 0).all()
+
+
 def ft_case(device, dtype, hq, hkv, d, positions, cap, seed):
     g = torch.Generator(device=device).manual_seed(seed)
     batch = len(positions)

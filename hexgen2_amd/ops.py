@@ -500,3 +500,48 @@ class DecodeStepGraph:
 
     def replay(self) -> None:
         self.graph.replay()
+
+
+class FtDecodeStepGraph:
+    """``DecodeStepGraph`` over FasterTransformer caches: one HIP graph per
+    decode step holding every layer's ``ft_attend`` (rotary, append at
+    ``positions``, attention over ``[0, positions]``) and the advance of
+    ``positions`` by one.  This is the layout the reference's CUDA-graph
+    decode captures (hexgen/hexgen_core/generation.py:354-443 requires
+    ``fused_ft_kernel``).  ``max_position`` bounds every position over every
+    replay and must stay below the caches' capacity.
+
+    As with ``DecodeStepGraph``, the kernels must have run once eagerly
+    before capture, and every captured tensor must stay alive and be updated
+    in place while the graph is replayed.
+    """
+
+    def __init__(self, q_layers: TensorList, k_cache_layers: TensorList, v_cache_layers: TensorList,
+                 out_layers: TensorList, k_new_layers: TensorList, v_new_layers: TensorList,
+                 positions: torch.Tensor, max_position: int, rotary_dim: int = 0,
+                 rotary_base: float = 10000.0, rotary_neox: bool = True,
+                 softmax_scale: Optional[float] = None):
+        self.q, self.out = _as_layers(q_layers), _as_layers(out_layers)
+        self.k_cache, self.v_cache = _as_layers(k_cache_layers), _as_layers(v_cache_layers)
+        self.k_new, self.v_new = _as_layers(k_new_layers), _as_layers(v_new_layers)
+        n = len(self.q)
+        if not n or any(len(x) != n for x in (self.out, self.k_cache, self.v_cache, self.k_new, self.v_new)):
+            raise ValueError("one q, out, K cache, V cache, k_new and v_new tensor per layer")
+        _require_device(positions)
+        if positions.dtype != torch.int32 or not positions.is_contiguous():
+            raise ValueError("positions must be a contiguous int32 device tensor")
+        self.positions, self.max_position = positions, int(max_position)
+        need = ft_attend_workspace_bytes(self.q[0], self.k_cache[0], self.v_cache[0], self.max_position)
+        self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=self.q[0].device)
+        self.args = dict(max_position=self.max_position, positions=positions, rotary_dim=rotary_dim,
+                         rotary_base=rotary_base, rotary_neox=rotary_neox, softmax_scale=softmax_scale,
+                         workspace=self.workspace)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            for l in range(n):
+                ft_attend(self.q[l], self.k_new[l], self.v_new[l], self.k_cache[l], self.v_cache[l],
+                          out=self.out[l], **self.args)
+            self.positions.add_(1)
+
+    def replay(self) -> None:
+        self.graph.replay()

@@ -63,3 +63,52 @@ def test_graph_replays_match_eager_steps(device, hq, hkv, d, dtype, kernel):
             # the step appended exactly one row per sequence
             changed = (cache_e[0] != before).flatten(2).any(-1)
             assert changed.sum() <= len(lens)
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,rot", [(32, 8, 128, torch.bfloat16, 128),
+                                                (8, 1, 64, torch.float16, 32),
+                                                (4, 4, 16, torch.float32, 0)])
+def test_ft_graph_replays_match_eager_steps(device, hq, hkv, d, dtype, rot):
+    """ops.FtDecodeStepGraph: every replay equals the eager ft_attend calls of
+    the same step bit for bit (caches, outputs, positions)."""
+    layers, lens, steps = 3, [1, 40, 300, 1029, 7], 5
+    cap = max(lens) + steps + 3
+    max_position = max(lens) + steps
+    batch = len(lens)
+    g = torch.Generator(device=device).manual_seed(22)
+    k_shape, v_shape = ops.ft_cache_shapes(batch, hkv, cap, d, dtype)
+    k_e = torch.randn((layers,) + k_shape, generator=g, device=device).to(dtype)
+    v_e = torch.randn((layers,) + v_shape, generator=g, device=device).to(dtype)
+    k_g, v_g = k_e.clone(), v_e.clone()
+    q = torch.empty((layers, batch, hq, d), dtype=dtype, device=device)
+    new = torch.empty((layers, 2, batch, hkv, d), dtype=dtype, device=device)
+    out_e = torch.empty_like(q)
+    out_g = torch.empty_like(q)
+    pos_e = torch.tensor(lens, dtype=torch.int32, device=device)
+    pos_g = pos_e.clone()
+
+    def eager_step():
+        for l in range(layers):
+            ops.ft_attend(q[l], new[l, 0], new[l, 1], k_e[l], v_e[l], max_position=max_position, positions=pos_e,
+                          rotary_dim=rot, out=out_e[l])
+        pos_e.add_(1)
+
+    def refill():
+        q.copy_(torch.randn(q.shape, generator=g, device=device).to(dtype))
+        new.copy_(torch.randn(new.shape, generator=g, device=device).to(dtype))
+
+    refill()
+    eager_step()  # also loads the kernels before capture
+    k_g.copy_(k_e)
+    v_g.copy_(v_e)
+    pos_g.copy_(pos_e)
+    torch.cuda.synchronize()
+    graph = ops.FtDecodeStepGraph(q, k_g, v_g, out_g, new[:, 0], new[:, 1], pos_g, max_position, rotary_dim=rot)
+    for step in range(steps - 1):
+        refill()
+        eager_step()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pos_g, pos_e)
+        assert torch.equal(k_g, k_e) and torch.equal(v_g, v_e), f"step {step}: caches differ"
+        assert torch.equal(out_g, out_e), f"step {step}: output differs"

@@ -6,7 +6,9 @@ cache, SwiGLU MLP, untied LM head; hexgen/hexgen_core/models/gpt.py:363-483,
 modules/block.py:112-175, mlp.py:63-87, rms_norm.py:6-15).  Weights are read
 in HuggingFace Llama layout from safetensors.  Per layer and step the cache
 calls are exactly the reference's: ``_update_kv_cache`` then
-``FlashCrossAttention`` (mha.py:565-569), or the fused HIP append+attend.
+``FlashCrossAttention`` (mha.py:565-569), or the fused HIP append+attend;
+with ``fused_ft_kernel`` the decode steps call
+``_apply_rotary_single_query_attention`` on unrotated q/k (mha.py:553-571).
 Dense projections use torch (hipBLASLt); every KV byte moves through hexkv.
 """
 from __future__ import annotations
@@ -18,7 +20,7 @@ from pathlib import Path
 import torch
 import torch.nn.functional as F
 
-from .mha import FlashCrossAttention, _update_kv_cache, update_and_attend
+from .mha import FlashCrossAttention, _apply_rotary_single_query_attention, _update_kv_cache, update_and_attend
 
 
 @dataclass
@@ -134,14 +136,19 @@ class LlamaHost:
             q = (x @ layer["wq"].T).view(batch, seqlen, s.num_attention_heads, d)
             k = (x @ layer["wk"].T).view(batch, seqlen, s.num_key_value_heads, d)
             v = (x @ layer["wv"].T).view(batch, seqlen, s.num_key_value_heads, d)
-            q, k = self._rope(q, offset), self._rope(k, offset)
-            kv = torch.stack((k, v), dim=2)  # [B, S, 2, Hkv, D]
-            if fused_append and offset > 0 and seqlen == 1 and i in inference_params.key_value_memory_dict:
-                context = update_and_attend(q, kv, inference_params, i, self.scale)
+            if inference_params.fused_ft_kernel and offset > 0:
+                # FT decode (mha.py:553-571): rotary, append and attention in one call
+                context = _apply_rotary_single_query_attention(q, inference_params, i, d, s.rope_theta,
+                                                               kv=torch.stack((k, v), dim=2))
             else:
-                kv_view = _update_kv_cache(kv, inference_params, i)
-                # prompt (offset 0): causal; decode: causal=False (mha.py:566-569)
-                context = self.attn(q, kv_view, causal=None if offset == 0 else False)
+                q, k = self._rope(q, offset), self._rope(k, offset)
+                kv = torch.stack((k, v), dim=2)  # [B, S, 2, Hkv, D]
+                if fused_append and offset > 0 and seqlen == 1 and i in inference_params.key_value_memory_dict:
+                    context = update_and_attend(q, kv, inference_params, i, self.scale)
+                else:
+                    kv_view = _update_kv_cache(kv, inference_params, i)
+                    # prompt (offset 0): causal; decode: causal=False (mha.py:566-569)
+                    context = self.attn(q, kv_view, causal=None if offset == 0 else False)
             h = h + context.reshape(batch, seqlen, -1) @ layer["wo"].T
             x = rms_norm(h, layer["ln2"], s.rms_norm_eps)
             h = h + (F.silu(x @ layer["gate"].T) * (x @ layer["up"].T)) @ layer["down"].T

@@ -81,3 +81,35 @@ def test_prefill_cache_is_one_packed_buffer(device):
     # layer 1 starts right after layer 0: one contiguous handoff buffer
     assert cache[1].data_ptr() == cache[0].data_ptr() + cache[0].numel() * cache[0].element_size()
     assert int(first) == int(logits.argmax(-1))
+
+
+def greedy_ft(host, prompt, count):
+    """The reference's fused_ft_kernel decode (generation.py:77-140 with
+    fused_ft_kernel=True): prefill writes the FT caches, every decode step
+    rotates, appends and attends in one FT call."""
+    from hexgen2_amd.generation import InferenceParams
+    params = InferenceParams(max_sequence_len=len(prompt) + count, max_batch_size=1, fused_ft_kernel=True)
+    logits = host.forward(torch.tensor([prompt], device="cuda"), params)
+    token = int(logits.argmax(-1))
+    tokens = [token]
+    params.sequence_len_offset = len(prompt)
+    for _ in range(count - 1):
+        logits = host.forward(torch.tensor([[token]], device="cuda"), params)
+        token = int(logits.argmax(-1))
+        tokens.append(token)
+        params.sequence_len_offset += 1
+    assert isinstance(params.key_value_memory_dict[0], tuple)  # the FT K/V pair
+    return tokens
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+def test_ft_decode_tokens_match_reference(device, dtype):
+    from hexgen2_amd.llama import LlamaHost
+    host = LlamaHost.load(GOLDEN / "fixture_seed17", "cuda", getattr(torch, dtype))
+    for case in GREEDY["fixture_seed17"]:
+        print(f"ft fixture {dtype} prompt={case['prompt']}", flush=True)
+        assert greedy_ft(host, case["prompt"], case["max_new_tokens"]) == case["reference_gpu_fp16_tokens"]
+    if dtype == "float32":
+        tiny = LlamaHost.load(GOLDEN / "tiny_llama", "cuda", torch.float32)
+        case = GREEDY["tiny_llama"][0]
+        assert greedy_ft(tiny, case["prompt"], case["max_new_tokens"]) == case["hf_fp32_tokens"]

@@ -111,10 +111,6 @@ __device__ __forceinline__ int row_length(const AttendArgs &a, int b, int t, int
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float readlane_f(float v, int lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
-}
-
 // What one workgroup does: query row (b, t), head group qh0.., KV head hk,
 // positions [p0, p0 + n) of which the first n_cache come from the cache and,
 // when has_new, the last one (pos_new) from kv_new.

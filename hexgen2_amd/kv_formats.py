@@ -24,6 +24,7 @@ hexkv decode path (per-sequence ``seqlens``) uses instead.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -36,13 +37,12 @@ from .ops import _require_device, _stream
 # --------------------------------------------------------------- blocks ---
 
 
-def _as_block(t: torch.Tensor, split: Optional[int] = None) -> Optional[_lib.Block]:
-    """Describe ``t`` as a hexkv block: rows are the dims from ``split`` on
-    (contiguous), indexed by the dims before it collapsed into at most two
-    strided levels (slices, rows).  ``split`` defaults to the start of the
-    longest contiguous trailing run.  Returns None when the layout needs
-    more levels or the row dims are not contiguous."""
-    shape, stride, elem = list(t.shape), list(t.stride()), t.element_size()
+@functools.lru_cache(maxsize=4096)
+def _layout(shape: Tuple[int, ...], stride: Tuple[int, ...], elem: int,
+            split: Optional[int]) -> Optional[Tuple[int, int, int, int, int]]:
+    """(width, height, depth, row_pitch, slice_pitch) in bytes of a tensor of
+    this shape and stride, or None; see ``_as_block``.  Cached: the layers of
+    one call usually share their shape and stride."""
     nd = len(shape)
     if split is None:
         split, expect = nd, 1
@@ -67,19 +67,43 @@ def _as_block(t: torch.Tensor, split: Optional[int] = None) -> Optional[_lib.Blo
     while len(merged) < 2:
         merged.insert(0, (1, 0))
     (depth, s_pitch), (height, r_pitch) = merged
-    if t.numel() == 0:
+    if 0 in shape:
         depth, height, width = 0, 0, 0
-    return _lib.Block(t.data_ptr(), width, height, depth, r_pitch * elem, s_pitch * elem)
+    return width, height, depth, r_pitch * elem, s_pitch * elem
 
 
-def _block(t: torch.Tensor, split: Optional[int] = None) -> Tuple[_lib.Block, torch.Tensor]:
-    """(block, tensor it describes): the tensor itself, or a contiguous copy
-    when its layout has no block description."""
-    b = _as_block(t, split)
-    if b is None:
+def _block_fields(t: torch.Tensor, split: Optional[int] = None) -> Optional[Tuple[int, ...]]:
+    """``hexkv_block`` fields (data, width, height, depth, row_pitch,
+    slice_pitch) of ``t``, or None; see ``_as_block``."""
+    lay = _layout(tuple(t.shape), t.stride(), t.element_size(), split)
+    return None if lay is None else (t.data_ptr(), *lay)
+
+
+def _as_block(t: torch.Tensor, split: Optional[int] = None) -> Optional[_lib.Block]:
+    """Describe ``t`` as a hexkv block: rows are the dims from ``split`` on
+    (contiguous), indexed by the dims before it collapsed into at most two
+    strided levels (slices, rows).  ``split`` defaults to the start of the
+    longest contiguous trailing run.  Returns None when the layout needs
+    more levels or the row dims are not contiguous."""
+    fields = _block_fields(t, split)
+    return None if fields is None else _lib.Block(*fields)
+
+
+def _block(t: torch.Tensor, split: Optional[int] = None) -> Tuple[Tuple[int, ...], torch.Tensor]:
+    """(block fields, tensor they describe): the tensor itself, or a
+    contiguous copy when its layout has no block description."""
+    fields = _block_fields(t, split)
+    if fields is None:
         t = t.contiguous()
-        b = _as_block(t, split)
-    return b, t
+        fields = _block_fields(t, split)
+    return fields, t
+
+
+def _block_array(fields: Sequence[Tuple[int, ...]]):
+    """A ``hexkv_block`` array of these fields, built in one allocation (the
+    struct is six 8-byte words: a pointer and five int64)."""
+    flat = [x for f in fields for x in f]
+    return ctypes.cast((ctypes.c_int64 * len(flat))(*flat), ctypes.POINTER(_lib.Block))
 
 
 def _one_dtype(tensors: Sequence[torch.Tensor], what: str) -> torch.dtype:
@@ -112,8 +136,7 @@ def flat_concat(tensors: Sequence[torch.Tensor], out: Optional[torch.Tensor] = N
         b, t = _block(t)
         keep.append(t)
         blocks.append(b)
-    rc = _lib.load().hexkv_flat_concat((_lib.Block * len(blocks))(*blocks), len(blocks), out.data_ptr(),
-                                       _stream(out))
+    rc = _lib.load().hexkv_flat_concat(_block_array(blocks), len(blocks), out.data_ptr(), _stream(out))
     _lib.check(rc, "hexkv_flat_concat")
     return out
 
@@ -232,13 +255,15 @@ def batch_key_value_memory_dicts(kv_memory_dicts_list: Sequence[Dict[int, torch.
     if any(t.dim() < 2 for t in first):
         raise ValueError("cache tensors must be [batch, positions, ...]")
     rest = tuple(first[0].shape[2:])
+    rest_size, heads, ragged = first[0].shape[2:], [t.shape[:2] for t in first], False
     for key in keys:
         for i, d in enumerate(dicts):
-            t = d[key]
-            if t.dim() < 2 or tuple(t.shape[2:]) != rest:
-                raise ValueError(f"request {i} layer {key}: shape {tuple(t.shape)} does not batch with "
+            shape = d[key].shape
+            if len(shape) < 2 or shape[2:] != rest_size:
+                raise ValueError(f"request {i} layer {key}: shape {tuple(shape)} does not batch with "
                                  f"rows of shape {rest}")
-    if any(d[key].shape[:2] != first[i].shape[:2] for key in keys for i, d in enumerate(dicts)):
+            ragged = ragged or shape[:2] != heads[i]
+    if ragged:
         # a request's sizes differ between layers: each key is padded to its
         # own longest request (kv_cache_batch.py:14), one launch per key
         out = {}
@@ -250,19 +275,25 @@ def batch_key_value_memory_dicts(kv_memory_dicts_list: Sequence[Dict[int, torch.
     seqs = sum(t.shape[0] for t in first)
     out = torch.empty((len(keys), seqs, max_rows, *rest), dtype=dtype, device=first[0].device)
     keep, blocks = [], []
-    width = math.prod(rest) * first[0].element_size()
+    elem = first[0].element_size()
+    width = math.prod(rest) * elem
+    # rows (dims 2+) are contiguous when every dim of size > 1 has its
+    # contiguous stride
+    row_dims = [d for d in range(len(rest)) if rest[d] != 1]
+    row_strides = tuple(math.prod(rest[d + 1:]) for d in row_dims)
     for key in keys:
         for d in dicts:
             t = d[key]
-            if t.numel() and _as_block(t, split=2) is None:
-                t = t.contiguous()  # rows (dims 2+) not contiguous
+            st = t.stride()
+            if tuple(st[2 + d] for d in row_dims) != row_strides and t.numel():
+                t = t.contiguous()
+                st = t.stride()
             # depth = the request's sequences, height = its positions
-            blocks.append(_lib.Block(t.data_ptr() if t.numel() else 0, width, t.shape[1], t.shape[0],
-                                     t.stride(1) * t.element_size(), t.stride(0) * t.element_size()))
+            b, n = t.shape[0], t.shape[1]
+            blocks.append((t.data_ptr() if b * n else 0, width, n, b, st[1] * elem, st[0] * elem))
             keep.append(t)
     dst = (ctypes.c_void_p * len(keys))(*[out[l].data_ptr() for l in range(len(keys))])
-    rc = _lib.load().hexkv_batch_pad((_lib.Block * len(blocks))(*blocks), len(keys), len(dicts), dst,
-                                     max_rows, _stream(out))
+    rc = _lib.load().hexkv_batch_pad(_block_array(blocks), len(keys), len(dicts), dst, max_rows, _stream(out))
     _lib.check(rc, "hexkv_batch_pad")
     return {key: out[l] for l, key in enumerate(keys)}
 
@@ -346,14 +377,13 @@ def _head_concat(layers: Sequence[Sequence[torch.Tensor]], outs: Sequence[torch.
     for shards in layers:
         for t in shards:
             if t.numel() == 0:  # no heads in this shard, or no rows at all
-                b = _lib.Block(0, math.prod(t.shape[dim:]) * t.element_size(), math.prod(t.shape[:dim]), 1, 0, 0)
+                b = (0, math.prod(t.shape[dim:]) * t.element_size(), math.prod(t.shape[:dim]), 1, 0, 0)
             else:
                 b, t = _block(t, split=dim)
             keep.append(t)
             blocks.append(b)
     dst = (ctypes.c_void_p * len(layers))(*[o.data_ptr() for o in outs])
-    rc = _lib.load().hexkv_head_concat((_lib.Block * len(blocks))(*blocks), len(layers), len(layers[0]), dst,
-                                       _stream(outs[0]))
+    rc = _lib.load().hexkv_head_concat(_block_array(blocks), len(layers), len(layers[0]), dst, _stream(outs[0]))
     _lib.check(rc, "hexkv_head_concat")
 
 

@@ -49,6 +49,8 @@ def to_device(int_array, dtype, device):
     (torch.float32, 2, 7, 7, 2, 16),
     (torch.bfloat16, 1, 1, 4, 1, 256),
     (torch.float16, 2, 0, 3, 2, 32),
+    (torch.bfloat16, 2, 600, 640, 3, 32),  # two full 256-position tiles + 88; 12 chunks: 8 + 4
+    (torch.float32, 1, 300, 301, 1, 16),   # 4 chunks per row: one partial chunk tile
 ])
 def test_ft_store_is_the_reference_layout(device, dtype, batch, seq, cap, hkv, d):
     print(f"ft_store {dtype} b={batch} s={seq} cap={cap} h={hkv} d={d}", flush=True)

@@ -71,6 +71,7 @@ struct DLManagedTensor {
 };
 
 constexpr int kMaxDims = 8;
+constexpr size_t kMaxIpcBytes = size_t(1) << 31;
 
 struct Wrapped {
   DLManagedTensor managed;
@@ -95,6 +96,11 @@ extern "C" int hexkv_ipc_export(const void *ptr, hexkv_ipc_handle *handle, uint6
   size_t size = 0;
   hipError_t err = hipMemGetAddressRange(&base, &size, const_cast<void *>(ptr));
   if (err != hipSuccess) return fail(HEXKV_EHIP, "hexkv_ipc_export: %s", hipGetErrorString(err));
+  // Mapping an allocation of 2 GiB or more in another process has not
+  // returned on this platform: refuse to hand out a handle for one.
+  if (size >= kMaxIpcBytes)
+    return fail(HEXKV_ERANGE, "hexkv_ipc_export: allocation of %zu bytes; exported allocations must be below 2 GiB",
+                size);
   hipIpcMemHandle_t h;
   err = hipIpcGetMemHandle(&h, base);
   if (err != hipSuccess) return fail(HEXKV_EHIP, "hexkv_ipc_export: %s", hipGetErrorString(err));

@@ -362,7 +362,8 @@ typedef struct hexkv_ipc_handle {
 } hexkv_ipc_handle;
 
 /* Handle of the device allocation containing `ptr`, the byte offset of `ptr`
- * in it, and the allocation's size. */
+ * in it, and the allocation's size.  HEXKV_ERANGE (no handle) when the
+ * allocation is 2 GiB or larger. */
 int hexkv_ipc_export(const void *ptr, hexkv_ipc_handle *handle, uint64_t *offset,
                      uint64_t *alloc_bytes);
 

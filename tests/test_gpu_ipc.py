@@ -69,3 +69,21 @@ def test_ipc_rejects_host_tensors(device):
     from hexgen2_amd.transport import IpcChannel
     with pytest.raises(ValueError, match="device tensors"):
         IpcChannel().send({"x": torch.zeros(3)}, {}, dst=1)
+
+
+def test_ipc_export_refuses_allocations_of_2_gib(device):
+    """The C ABI itself refuses a handle for an allocation that another
+    process could not map (2 GiB or more), before any mapping is tried."""
+    import ctypes
+    from hexgen2_amd import _lib
+    lib = _lib.load()
+    handle, off, size = _lib.IpcHandle(), ctypes.c_uint64(), ctypes.c_uint64()
+    big = torch.empty(2 * 1024 ** 3, dtype=torch.uint8, device=device)
+    rc = lib.hexkv_ipc_export(ctypes.c_void_p(big.data_ptr() + 4096), ctypes.byref(handle), ctypes.byref(off),
+                              ctypes.byref(size))
+    assert rc == _lib.HEXKV_ERANGE and b"below 2 GiB" in lib.hexkv_last_error()
+    del big
+    small = torch.empty(1 << 20, dtype=torch.uint8, device=device)
+    rc = lib.hexkv_ipc_export(ctypes.c_void_p(small.data_ptr() + 256), ctypes.byref(handle), ctypes.byref(off),
+                              ctypes.byref(size))
+    assert rc == 0 and off.value >= 256 and size.value >= (1 << 20)

@@ -11,7 +11,10 @@ Inputs are resident in HBM before the timed region.
 Prints one JSON line: ``value`` = pack+unpack GB/s (algorithmic bytes), with
 the decode append+attend time per step, the roofline of the dominant kernel
 (decode attention) and the CPU baseline (the reference's PyTorch ops on this
-host's cores, on a bounded sample of the same workload).
+host's cores, on a bounded sample of the same workload).  Secondary figures
+outside the timed steps: ``formats`` (the legacy KV formats) and
+``ft_layout`` (the FasterTransformer cache layout), each with a ``cpu``
+entry timed the same way.
 """
 from __future__ import annotations
 
@@ -23,6 +26,7 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
 import torch
 
 ROOT = Path(__file__).resolve().parent
@@ -273,6 +277,75 @@ def measure_ft(device, steps=16):
     return out
 
 
+def _best_of(n, fn):
+    best = float("inf")
+    for _ in range(n):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def cpu_formats(cores):
+    """CPU figures beside ``measure_formats``: the reference's torch ops for
+    each legacy format (oracle/cpu_path.py) on host tensors of
+    ``format_cases``' shapes cut to 2 layers, GB/s with its byte accounting
+    (best of 2 calls; outputs allocated per call, as the reference does)."""
+    from oracle import cpu_path
+
+    torch.set_num_threads(cores)
+    row, L, bf = 2 * 8 * 128 * 2, 2, torch.bfloat16
+    out = {}
+    cache = torch.ones((L, 1, 8448, 2, 8, 128), dtype=bf)
+    layers = [cache[l, :, :8192] for l in range(L)]
+    sec = _best_of(2, lambda: cpu_path.flat_concat(layers))
+    out["flat_packet"] = 2 * L * 8192 * row / sec / 1e9
+    lens = [int(x) for x in torch.randint(128, 4097, (8,), generator=torch.Generator().manual_seed(0))]
+    bcache = torch.ones((L, 8, 4096, 2, 8, 128), dtype=bf)
+    dicts = [{l: bcache[l, i:i + 1, :n] for l in range(L)} for i, n in enumerate(lens)]
+    sec = _best_of(2, lambda: cpu_path.batch_pad(dicts))
+    out["zero_pad_batch"] = L * row * (sum(lens) + 8 * max(lens)) / sec / 1e9
+    shards_t = torch.ones((8, L, 8, 4096, 2, 1, 128), dtype=bf)
+    shards = [{l: shards_t[j, l] for l in range(L)} for j in range(8)]
+    sec = _best_of(2, lambda: cpu_path.concat_dicts(shards))
+    out["tp_head_concat"] = 2 * shards_t.numel() * 2 / sec / 1e9
+    return {k: {"gbs": round(v, 2), "cores": cores, "kind": "port",
+                "sample": "the reference's torch ops on 2 layers of the same shapes"} for k, v in out.items()}
+
+
+def cpu_ft(cores, w):
+    """CPU figures beside ``measure_ft``: the reference's FT prefill write
+    (oracle/cpu_path.py ft_store, mha.py:301-306) on 4 of the 64 sequences,
+    GB/s; and one FT decode step of the oracle's restatement (the reference
+    has no CPU path for it: ft_attention is a CUDA extension) on 2 sequences,
+    scaled by attended positions to the whole batch, µs per layer."""
+    from oracle import cpu_path, kv_oracle
+
+    torch.set_num_threads(cores)
+    B, H, Hq, D, dtype = 4, w.kv_heads, w.q_heads, w.head_dim, w.dtype
+    kv = torch.ones((B, 4096, 2, H, D), dtype=dtype)
+    k_shape, v_shape = ops.ft_cache_shapes(B, H, 4096, D, dtype)
+    k_cache, v_cache = torch.zeros(k_shape, dtype=dtype), torch.zeros(v_shape, dtype=dtype)
+    sec = _best_of(2, lambda: cpu_path.ft_store(kv, k_cache, v_cache))
+    store_gbs = 2 * kv.numel() * kv.element_size() / sec / 1e9
+    nb = 2
+    rng = np.random.default_rng(w.seed)
+    cap = max(w.lens[:nb]) + 1
+    k_ft = rng.standard_normal((nb, H, D // 8, cap, 8)).astype(np.float32)
+    v_ft = rng.standard_normal((nb, H, cap, D)).astype(np.float32)
+    q = rng.standard_normal((nb, Hq, D)).astype(np.float32)
+    new = rng.standard_normal((nb, 2, H, D)).astype(np.float32)
+    t0 = time.perf_counter()
+    kv_oracle.ft_decode(q, new[:, 0], new[:, 1], k_ft, v_ft, w.lens[:nb], rot_dim=D, dtype="bfloat16")
+    sec = time.perf_counter() - t0
+    scale = sum(n + 1 for n in w.lens) / sum(n + 1 for n in w.lens[:nb])
+    return ({"gbs": round(store_gbs, 2), "cores": cores, "kind": "port",
+             "sample": "the reference's FT write (mha.py:301-306) of 4 x 4096 positions"},
+            {"us_per_layer": round(sec * scale * 1e6, 1), "cores": 1, "kind": "port",
+             "sample": f"the oracle's FT decode step (numpy, fp64) on {nb} sequences, scaled x{scale:.1f} "
+                       "(attended positions)"})
+
+
 def cpu_baseline(w, job, budget_s):
     """The reference's PyTorch ops (oracle/cpu_path.py) on host cores, on a
     bounded sample: 2 layers of pack+unpack and 1 layer x a few decode steps
@@ -449,6 +522,14 @@ def main():
         log(f"legacy formats {result['formats']}")
         result["ft_layout"] = measure_ft(device)
         log(f"FT layout {result['ft_layout']}")
+        if not args.no_cpu_baseline:
+            cores = result["cpu_baseline"]["cores"]
+            for name, cpu in cpu_formats(cores).items():
+                result["formats"][name]["cpu"] = cpu
+            store_cpu, attend_cpu = cpu_ft(cores, workload("llama3-8b"))
+            result["ft_layout"]["ft_store"]["cpu"] = store_cpu
+            result["ft_layout"]["ft_attend"]["cpu"] = attend_cpu
+            log(f"CPU formats and FT {result['formats']} {result['ft_layout']}")
     print(json.dumps(result), flush=True)
 
 

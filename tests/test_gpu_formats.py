@@ -6,7 +6,6 @@ Geometries: the reference scripts' own example shapes (scaled where noted),
 the Llama geometries of the data path, strided cache views, layouts that
 force the 4- and 2-byte vector paths, empty requests and shards, rows longer
 than one tile, and more spans than one launch carries."""
-import os
 from datetime import timedelta
 from pathlib import Path
 

@@ -87,3 +87,23 @@ def test_ipc_export_refuses_allocations_of_2_gib(device):
     rc = lib.hexkv_ipc_export(ctypes.c_void_p(small.data_ptr() + 256), ctypes.byref(handle), ctypes.byref(off),
                               ctypes.byref(size))
     assert rc == 0 and off.value >= 256 and size.value >= (1 << 20)
+
+
+def test_handoff_bench_runs_and_delivers_bit_exact():
+    """python -m hexgen2_amd.handoff_bench on the tiny workload: two rounds,
+    each rank reports, and the decode rank's unpack from the peer's memory
+    is bit-exact on the sampled sequence."""
+    import json
+    import subprocess
+    import sys
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ, HSA_ENABLE_IPC_MODE_LEGACY="0")
+    print("handoff_bench tiny-llama, 2 rounds", flush=True)
+    result = subprocess.run([sys.executable, "-m", "hexgen2_amd.handoff_bench", "--workload", "tiny-llama",
+                             "--rounds", "2"], cwd=root, env=env, capture_output=True, text=True, timeout=100)
+    assert result.returncode == 0, result.stderr[-2000:]
+    lines = [json.loads(l) for l in result.stdout.splitlines() if l.startswith("{")]
+    decode = [l for l in lines if l["rank"] == 1]
+    assert sorted(l["round"] for l in lines if l["rank"] == 0) == [0, 1]
+    assert [l["round"] for l in decode] == [0, 1]
+    assert all(l["sampled_sequence_bit_exact"] and l["handoff_ms"] > 0 for l in decode)

@@ -53,7 +53,13 @@ rot_dim 0 are the identity, every pair keeps its norm, a 2-vector turns by
 pos radians) and, for the GPT-NeoX form, against transformers' Llama
 ``apply_rotary_pos_emb``, with the GPT-J form tied to it by the pair
 permutation; ``round_to`` against torch's casts; ``ft_decode`` without
-rotation against ``append`` + ``attend``.
+rotation against ``append`` + ``attend``.  One detail of ``ft_decode`` is
+parity unpinned: the point where the rotated q and k are rounded to the data
+type (after the rotation, before the products; the rotated k is what the
+cache keeps).  It follows FasterTransformer's published masked-attention
+kernel, which ft_attention wraps, but no output of that extension exists to
+check it against; its effect is one rounding of q and k (within the
+attention tolerances either way).
 """
 from __future__ import annotations
 

@@ -53,21 +53,33 @@ struct SpanArgs {
 };
 static_assert(sizeof(SpanArgs) <= 4096, "kernel arguments above 4 KiB");
 
-// A wide row piece: the workgroup strides along it.
+// A wide row piece: the workgroup strides along it.  A zero fill (no
+// source) has its own loop with eight stores in flight per lane: on MI355X
+// zero-pad batching moved 5.12 TB/s with it against 5.05 with the copy loop
+// storing zeros, and the copy loop without the per-element source test moved
+// the flat packet at 5.72 against 5.63.
 template <typename V>
 __device__ __forceinline__ void move_row(const char *__restrict__ s, char *__restrict__ d, int64_t nv) {
   const V *sv = reinterpret_cast<const V *>(s);
   V *dv = reinterpret_cast<V *>(d);
   int64_t i = threadIdx.x;
+  if (!sv) {
+    constexpr int kZeroUnroll = 8;
+    for (; i + (kZeroUnroll - 1) * kSpanThreads < nv; i += kZeroUnroll * kSpanThreads) {
+#pragma unroll
+      for (int u = 0; u < kZeroUnroll; ++u) __builtin_nontemporal_store(V{}, dv + i + u * kSpanThreads);
+    }
+    for (; i < nv; i += kSpanThreads) __builtin_nontemporal_store(V{}, dv + i);
+    return;
+  }
   for (; i + (kSpanUnroll - 1) * kSpanThreads < nv; i += kSpanUnroll * kSpanThreads) {
     V r[kSpanUnroll];
 #pragma unroll
-    for (int u = 0; u < kSpanUnroll; ++u)
-      r[u] = sv ? __builtin_nontemporal_load(sv + i + u * kSpanThreads) : V{};
+    for (int u = 0; u < kSpanUnroll; ++u) r[u] = __builtin_nontemporal_load(sv + i + u * kSpanThreads);
 #pragma unroll
     for (int u = 0; u < kSpanUnroll; ++u) __builtin_nontemporal_store(r[u], dv + i + u * kSpanThreads);
   }
-  for (; i < nv; i += kSpanThreads) __builtin_nontemporal_store(sv ? __builtin_nontemporal_load(sv + i) : V{}, dv + i);
+  for (; i < nv; i += kSpanThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(sv + i), dv + i);
 }
 
 template <typename V>

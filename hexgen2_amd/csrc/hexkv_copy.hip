@@ -11,7 +11,7 @@
 //    crosses at most a few sequence boundaries, found by one scalar binary
 //    search per workgroup;
 //  * each lane moves 16-byte vectors with nontemporal (streaming) loads and
-//    stores, four in flight per lane, so the 256 MB MALL is not polluted by
+//    stores, eight in flight per lane, so the 256 MB MALL is not polluted by
 //    data that is touched exactly once.
 #include "hexkv_common.h"
 
@@ -19,15 +19,20 @@
 
 namespace hexkv {
 
-// 512 threads x 4 vectors of 16 bytes in flight per workgroup, chunks of at
-// most 128 KB.  Measured on MI355X with the Llama-3-8B handoff (pack + unpack
-// of 2 x 63.9 GB): 23.24-23.32 ms against 23.48-23.50 for 256 threads and
-// 256 KB chunks, 24.1 for 512 threads and 256 KB, 23.8 for 1024 x 2.  For
-// reference a plain chunked copy reaches 5.55-5.76 TB/s (read + write), a
+// 1024 threads x 8 vectors of 16 bytes in flight per workgroup: a whole
+// 128 KB chunk is loaded before any of it is stored.  Measured on MI355X
+// with the Llama-3-8B handoff (pack + unpack of 2 x 63.9 GB), every variant
+// on the same buffers in one process (medians of 4-5 interleaved rounds):
+// 1024 x 8 21.15 ms; 512 x 8 22.2; 512 x 16 22.5; 1024 x 8 with 256 KB
+// chunks 21.4, with 64 KB 22.4; 1024 x 4 21.9; 1024 x 16 with 256 KB 21.9;
+// 512 x 4 (the earlier choice) 23.3; 256 x 8 23.6.  For reference a plain
+// chunked copy of 512 x 4 reached 5.55-5.76 TB/s (read + write), a
 // device-to-device hipMemcpy 4.90, a write-only stream 6.2-6.4 and a
 // read-only stream 7.1.
-constexpr int kCopyThreads = 512;
-constexpr int kCopyUnroll = 4;
+constexpr int kCopyThreads = 1024;
+constexpr int kCopyUnroll = 8;
+// The per-step append moves one row per sequence: 512 threads, one vector each.
+constexpr int kAppendThreads = 512;
 
 struct RaggedCopyArgs {
   const char *src[HEXKV_MAX_LAYERS_PER_LAUNCH];
@@ -95,7 +100,7 @@ __global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const RaggedC
 }
 
 template <typename V>
-__global__ __launch_bounds__(kCopyThreads) void append_kernel(
+__global__ __launch_bounds__(kAppendThreads) void append_kernel(
     const char *__restrict__ kv_new, char *__restrict__ cache, int64_t seq_stride_bytes,
     int64_t capacity, int64_t row_bytes, const int32_t *__restrict__ positions, int32_t bias) {
   const int b = blockIdx.y;
@@ -104,8 +109,8 @@ __global__ __launch_bounds__(kCopyThreads) void append_kernel(
   const int64_t nv = row_bytes / static_cast<int64_t>(sizeof(V));
   const V *s = reinterpret_cast<const V *>(kv_new + b * row_bytes);
   V *d = reinterpret_cast<V *>(cache + b * seq_stride_bytes + pos * row_bytes);
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kCopyThreads + threadIdx.x; i < nv;
-       i += static_cast<int64_t>(gridDim.x) * kCopyThreads)
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kAppendThreads + threadIdx.x; i < nv;
+       i += static_cast<int64_t>(gridDim.x) * kAppendThreads)
     d[i] = s[i];
 }
 
@@ -230,15 +235,15 @@ extern "C" int hexkv_append(const void *kv_new, void *cache, int batch, int64_t 
     return fail(HEXKV_EINVAL, "hexkv_append: pointers not 4-byte aligned");
   const bool vec16 = row_bytes % 16 == 0 && aligned16(kv_new) && aligned16(cache);
   const int64_t nv = row_bytes / (vec16 ? 16 : 4);
-  const unsigned gx = static_cast<unsigned>(std::min<int64_t>((nv + kCopyThreads - 1) / kCopyThreads, 64));
+  const unsigned gx = static_cast<unsigned>(std::min<int64_t>((nv + kAppendThreads - 1) / kAppendThreads, 64));
   dim3 grid(gx, static_cast<unsigned>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t stride = seq_stride_rows * row_bytes;
   if (vec16)
-    append_kernel<u32x4><<<grid, kCopyThreads, 0, s>>>(static_cast<const char *>(kv_new),
+    append_kernel<u32x4><<<grid, kAppendThreads, 0, s>>>(static_cast<const char *>(kv_new),
         static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias);
   else
-    append_kernel<unsigned int><<<grid, kCopyThreads, 0, s>>>(static_cast<const char *>(kv_new),
+    append_kernel<unsigned int><<<grid, kAppendThreads, 0, s>>>(static_cast<const char *>(kv_new),
         static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias);
   return check_launch("hexkv_append");
 }

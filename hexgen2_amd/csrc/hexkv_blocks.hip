@@ -12,9 +12,10 @@
 // views of one stacked allocation), the layers fold into a fourth dimension
 // of each span and one launch moves them all.  One workgroup moves one tile with
 // nontemporal 16-byte loads and stores (narrower vectors only when an
-// address, pitch or width is not a multiple of 16), four in flight per lane;
-// short rows are spread over the workgroup several per pass, so a 256-byte
-// head slice keeps every lane busy.  The tile -> span lookup is one scalar
+// address, pitch or width is not a multiple of 16): eight in flight per lane
+// when every tile of the launch is a wide row, four otherwise, where short
+// rows are spread over the workgroup several per pass, so a 256-byte head
+// slice keeps every lane busy.  The tile -> span lookup is one scalar
 // binary search over the prefix sums of tile counts.
 #include "hexkv_common.h"
 
@@ -23,13 +24,20 @@
 
 namespace hexkv {
 
-// 512 threads and tiles of at most 128 KB, as for the ragged copy: on MI355X
-// the flat packet moved 5.61 TB/s against 5.34 with 256 threads and 256 KB
-// tiles, zero-pad batching 5.03 against 4.84, TP head concatenation 5.15
-// against 5.08.  The FT store keeps 256 threads (its tile shape is its own).
+// Tiles of at most 128 KB.  A launch whose tiles are all wide rows (at least
+// kWideThreads vectors) runs kWideThreads threads with kWideUnroll vectors in
+// flight per lane, a whole tile loaded before it is stored, as the ragged
+// copy does; any other launch runs kSpanThreads x kSpanUnroll, which spreads
+// short rows over the workgroup.  On MI355X (all variants on the same
+// buffers in one process): flat packet 6.02 TB/s with 1024 x 8 against 5.72
+// with 512 x 4, zero-pad batching 5.47 against 5.11, but TP head
+// concatenation (256-byte rows) 4.87 against 5.17.  The FT store keeps 256
+// threads (its tile shape is its own).
 constexpr int kSpanThreads = 512;
-constexpr int kFtThreads = 256;
 constexpr int kSpanUnroll = 4;
+constexpr int kWideThreads = 1024;
+constexpr int kWideUnroll = 8;
+constexpr int kFtThreads = 256;
 constexpr int kMaxSpans = 32;
 
 struct Span {
@@ -58,32 +66,32 @@ static_assert(sizeof(SpanArgs) <= 4096, "kernel arguments above 4 KiB");
 // zero-pad batching moved 5.12 TB/s with it against 5.05 with the copy loop
 // storing zeros, and the copy loop without the per-element source test moved
 // the flat packet at 5.72 against 5.63.
-template <typename V>
+template <typename V, int T, int UR>
 __device__ __forceinline__ void move_row(const char *__restrict__ s, char *__restrict__ d, int64_t nv) {
   const V *sv = reinterpret_cast<const V *>(s);
   V *dv = reinterpret_cast<V *>(d);
   int64_t i = threadIdx.x;
   if (!sv) {
     constexpr int kZeroUnroll = 8;
-    for (; i + (kZeroUnroll - 1) * kSpanThreads < nv; i += kZeroUnroll * kSpanThreads) {
+    for (; i + (kZeroUnroll - 1) * T < nv; i += kZeroUnroll * T) {
 #pragma unroll
-      for (int u = 0; u < kZeroUnroll; ++u) __builtin_nontemporal_store(V{}, dv + i + u * kSpanThreads);
+      for (int u = 0; u < kZeroUnroll; ++u) __builtin_nontemporal_store(V{}, dv + i + u * T);
     }
-    for (; i < nv; i += kSpanThreads) __builtin_nontemporal_store(V{}, dv + i);
+    for (; i < nv; i += T) __builtin_nontemporal_store(V{}, dv + i);
     return;
   }
-  for (; i + (kSpanUnroll - 1) * kSpanThreads < nv; i += kSpanUnroll * kSpanThreads) {
-    V r[kSpanUnroll];
+  for (; i + (UR - 1) * T < nv; i += UR * T) {
+    V r[UR];
 #pragma unroll
-    for (int u = 0; u < kSpanUnroll; ++u) r[u] = __builtin_nontemporal_load(sv + i + u * kSpanThreads);
+    for (int u = 0; u < UR; ++u) r[u] = __builtin_nontemporal_load(sv + i + u * T);
 #pragma unroll
-    for (int u = 0; u < kSpanUnroll; ++u) __builtin_nontemporal_store(r[u], dv + i + u * kSpanThreads);
+    for (int u = 0; u < UR; ++u) __builtin_nontemporal_store(r[u], dv + i + u * T);
   }
-  for (; i < nv; i += kSpanThreads) __builtin_nontemporal_store(__builtin_nontemporal_load(sv + i), dv + i);
+  for (; i < nv; i += T) __builtin_nontemporal_store(__builtin_nontemporal_load(sv + i), dv + i);
 }
 
-template <typename V>
-__global__ __launch_bounds__(kSpanThreads) void span_copy_kernel(const SpanArgs a) {
+template <typename V, int T, int UR>
+__global__ __launch_bounds__(T) void span_copy_kernel(const SpanArgs a) {
   const int tile = blockIdx.x;
   int lo = 0, hi = a.n;
   while (hi - lo > 1) {
@@ -104,27 +112,27 @@ __global__ __launch_bounds__(kSpanThreads) void span_copy_kernel(const SpanArgs 
   const int64_t nv = (min(s.width, c0 + s.tile_cols) - c0) / static_cast<int64_t>(sizeof(V));
   const char *src = s.src ? s.src + m * s.src_layer + k * s.src_slice + c0 : nullptr;
   char *dst = s.dst + m * s.dst_layer + k * s.dst_slice + c0;
-  if (nv >= kSpanThreads) {
+  if (nv >= T) {
     for (int r = r0; r < r1; ++r)
-      move_row<V>(src ? src + r * s.src_row : nullptr, dst + r * s.dst_row, nv);
+      move_row<V, T, UR>(src ? src + r * s.src_row : nullptr, dst + r * s.dst_row, nv);
     return;
   }
   // Short rows: `per` rows per pass, lane (tr, tc) = (row in pass, vector).
-  const int per = kSpanThreads / static_cast<int>(nv);
+  const int per = T / static_cast<int>(nv);
   const int tr = threadIdx.x / static_cast<int>(nv);
   const int tc = threadIdx.x - tr * static_cast<int>(nv);
   if (tr >= per) return;
   const int64_t col = static_cast<int64_t>(tc) * static_cast<int64_t>(sizeof(V));
-  for (int r = r0 + tr; r < r1; r += per * kSpanUnroll) {
-    V v[kSpanUnroll];
+  for (int r = r0 + tr; r < r1; r += per * UR) {
+    V v[UR];
 #pragma unroll
-    for (int u = 0; u < kSpanUnroll; ++u) {
+    for (int u = 0; u < UR; ++u) {
       const int rr = r + u * per;
       v[u] = V{};
       if (src && rr < r1) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V *>(src + rr * s.src_row + col));
     }
 #pragma unroll
-    for (int u = 0; u < kSpanUnroll; ++u) {
+    for (int u = 0; u < UR; ++u) {
       const int rr = r + u * per;
       if (rr < r1) __builtin_nontemporal_store(v[u], reinterpret_cast<V *>(dst + rr * s.dst_row + col));
     }
@@ -270,8 +278,9 @@ static int64_t tile_bytes(int64_t total) {
 }
 
 template <typename V>
-static void launch_spans(const SpanArgs &a, int tiles, hipStream_t s) {
-  span_copy_kernel<V><<<dim3(static_cast<unsigned>(tiles)), kSpanThreads, 0, s>>>(a);
+static void launch_spans(const SpanArgs &a, int tiles, bool wide, hipStream_t s) {
+  if (wide) span_copy_kernel<V, kWideThreads, kWideUnroll><<<dim3(static_cast<unsigned>(tiles)), kWideThreads, 0, s>>>(a);
+  else span_copy_kernel<V, kSpanThreads, kSpanUnroll><<<dim3(static_cast<unsigned>(tiles)), kSpanThreads, 0, s>>>(a);
 }
 
 // Moves every span, kMaxSpans per launch, in order on `stream`.
@@ -344,11 +353,14 @@ static int run_moves(std::vector<Move> &moves, hipStream_t stream, const char *w
     }
     a.first_tile[n] = static_cast<int32_t>(tiles);
     a.n = n;
+    // Wide launch: every span's tiles are rows of at least kWideThreads vectors.
+    bool wide = true;
+    for (int q = 0; q < n; ++q) wide = wide && a.span[q].tile_cols >= static_cast<int64_t>(kWideThreads) * vec;
     switch (vec) {
-      case 16: launch_spans<u32x4>(a, static_cast<int>(tiles), stream); break;
-      case 4: launch_spans<unsigned int>(a, static_cast<int>(tiles), stream); break;
-      case 2: launch_spans<unsigned short>(a, static_cast<int>(tiles), stream); break;
-      default: launch_spans<unsigned char>(a, static_cast<int>(tiles), stream); break;
+      case 16: launch_spans<u32x4>(a, static_cast<int>(tiles), wide, stream); break;
+      case 4: launch_spans<unsigned int>(a, static_cast<int>(tiles), wide, stream); break;
+      case 2: launch_spans<unsigned short>(a, static_cast<int>(tiles), wide, stream); break;
+      default: launch_spans<unsigned char>(a, static_cast<int>(tiles), wide, stream); break;
     }
     const int rc = check_launch(what);
     if (rc != HEXKV_OK) return rc;

@@ -31,13 +31,13 @@ namespace hexkv {
 // short rows over the workgroup.  On MI355X (all variants on the same
 // buffers in one process): flat packet 6.02 TB/s with 1024 x 8 against 5.72
 // with 512 x 4, zero-pad batching 5.47 against 5.11, but TP head
-// concatenation (256-byte rows) 4.87 against 5.17.  The FT store keeps 256
-// threads (its tile shape is its own).
+// concatenation (256-byte rows) 4.87 against 5.17.  The FT store has its own
+// thread count and tile shape.
 constexpr int kSpanThreads = 512;
 constexpr int kSpanUnroll = 4;
 constexpr int kWideThreads = 1024;
 constexpr int kWideUnroll = 8;
-constexpr int kFtThreads = 256;
+constexpr int kFtThreads = 1024;
 constexpr int kMaxSpans = 32;
 
 struct Span {
@@ -145,9 +145,11 @@ __global__ __launch_bounds__(T) void span_copy_kernel(const SpanArgs a) {
 // pieces) into LDS and writes them out plane by plane (kFtRows x 16-byte
 // runs); the V chunks go straight from the rows to their head rows.  Long
 // plane runs matter more than long row reads: on MI355X with a 64 x 4096
-// position Llama-3-8B prefill, 16 x 128 tiles moved 4.0 TB/s, 64 x 32 5.1,
-// 128 x 16 5.4 and 256 x 8 5.6 (the plain-copy ceiling).
-constexpr int kFtRows = 256, kFtCols = 8;
+// position Llama-3-8B prefill and 256 threads, 16 x 128 tiles moved 4.0
+// TB/s, 64 x 32 5.1, 128 x 16 5.4 and 256 x 8 5.6; 1024 threads on 512 x 8
+// tiles take 0.374 ms against 0.384 for 256 on 256 x 8 (5.74 TB/s; 512
+// threads on 256 x 8 0.398, on 512 x 8 0.376; 1024 on 1024 x 8 0.410).
+constexpr int kFtRows = 512, kFtCols = 8;
 
 struct FtStoreArgs {
   const char *src;  // K of sequence 0, position 0

@@ -139,6 +139,55 @@ __global__ __launch_bounds__(T) void span_copy_kernel(const SpanArgs a) {
   }
 }
 
+// Head concatenation as a gather (hexkv_head_concat's fast path): a
+// workgroup takes a tile of destination rows and its lanes lie across one
+// destination row, each lane in the shard its column falls in; every pass
+// loads kWideUnroll rows per lane from the shards' own rows, then stores the
+// whole destination rows.  Reads stay contiguous per shard, writes become
+// whole-row runs instead of one shard's slice per row (the span engine
+// writes 256-byte pieces 2 KB apart for eight one-head shards).
+constexpr int kGatherShards = 16;
+
+struct GatherArgs {
+  const char *src[kGatherShards];
+  int64_t src_pitch[kGatherShards];   // bytes between a shard's rows
+  int64_t src_layer[kGatherShards];   // bytes between a shard's layers
+  int32_t vec_start[kGatherShards + 1];  // first 16-byte column of each shard
+  char *dst;
+  int64_t dst_layer;
+  int64_t rows;           // rows per layer
+  int32_t wvec;           // 16-byte vectors per destination row (<= kWideThreads)
+  int32_t n;              // shards
+  int32_t rows_per_tile;
+};
+
+__global__ __launch_bounds__(kWideThreads) void head_gather_kernel(const GatherArgs a) {
+  const int64_t l = blockIdx.y;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_tile;
+  const int64_t r1 = min(a.rows, r0 + a.rows_per_tile);
+  const int per = kWideThreads / a.wvec;  // destination rows per pass
+  const int tr = threadIdx.x / a.wvec, tc = threadIdx.x - tr * a.wvec;
+  if (tr >= per) return;
+  int j = 0;
+  while (j + 1 < a.n && a.vec_start[j + 1] <= tc) ++j;
+  const char *src = a.src[j] + l * a.src_layer[j] + static_cast<int64_t>(tc - a.vec_start[j]) * 16;
+  const int64_t sp = a.src_pitch[j], dp = static_cast<int64_t>(a.wvec) * 16;
+  char *dst = a.dst + l * a.dst_layer + static_cast<int64_t>(tc) * 16;
+  for (int64_t r = r0 + tr; r < r1; r += static_cast<int64_t>(per) * kWideUnroll) {
+    u32x4 v[kWideUnroll];
+#pragma unroll
+    for (int u = 0; u < kWideUnroll; ++u) {
+      const int64_t rr = min(r + u * per, r1 - 1);
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + rr * sp));
+    }
+#pragma unroll
+    for (int u = 0; u < kWideUnroll; ++u) {
+      const int64_t rr = r + u * per;
+      if (rr < r1) __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4 *>(dst + rr * dp));
+    }
+  }
+}
+
 // FT store (hexkv_ft_store): kv rows [2][H][D] -> K chunk planes and
 // head-major V.  A workgroup takes up to kFtRows positions x kFtCols 16-byte
 // chunks of one sequence: it reads the K chunks row by row (kFtCols x 16-byte
@@ -370,6 +419,65 @@ static int run_moves(std::vector<Move> &moves, hipStream_t stream, const char *w
   return HEXKV_OK;
 }
 
+// hexkv_head_concat through head_gather_kernel when the shapes allow it
+// (validated blocks): at most kGatherShards shards, destination rows of at
+// most kWideThreads 16-byte vectors, every shard's rows one level (depth 1,
+// or slices that follow each other) with 16-byte aligned data and pitch,
+// every layer holding rows.  Layers whose pointers advance by fixed strides
+// share one launch; otherwise one launch per layer.  Returns false (nothing
+// launched) when the shapes do not qualify.
+static bool head_gather(const hexkv_block *src, int n_layers, int n_shards, void *const *dst_layers, int64_t row,
+                        hipStream_t stream) {
+  if (n_shards > kGatherShards || row <= 0 || row % 16 || row / 16 > kWideThreads) return false;
+  const int64_t rows = src[0].depth * src[0].height;
+  if (rows <= 0 || rows > INT64_C(1) << 40) return false;
+  // Bytes between consecutive rows of a one-level block.
+  const auto pitch = [](const hexkv_block &b) { return b.height > 1 || b.depth == 1 ? b.row_pitch : b.slice_pitch; };
+  for (int l = 0; l < n_layers; ++l) {
+    if (!dst_layers[l] || !aligned16(dst_layers[l])) return false;
+    for (int j = 0; j < n_shards; ++j) {
+      const hexkv_block &b = src[static_cast<int64_t>(l) * n_shards + j];
+      if (b.depth * b.height != rows || b.width % 16) return false;
+      if (b.width == 0) continue;
+      if (!aligned16(b.data) || b.row_pitch % 16) return false;
+      if (b.depth > 1 && b.slice_pitch != b.height * b.row_pitch) return false;
+      if (pitch(b) != pitch(src[j])) return false;  // one pitch per shard over every layer
+    }
+  }
+  GatherArgs a{};
+  a.n = n_shards;
+  a.wvec = static_cast<int32_t>(row / 16);
+  a.rows = rows;
+  a.rows_per_tile = static_cast<int32_t>(std::max<int64_t>(1, 131072 / row));
+  a.vec_start[0] = 0;
+  for (int j = 0; j < n_shards; ++j) {
+    a.vec_start[j + 1] = a.vec_start[j] + static_cast<int32_t>(src[j].width / 16);
+    a.src_pitch[j] = pitch(src[j]);
+  }
+  // One launch for every layer when the layers advance by fixed strides.
+  bool fold = n_layers > 1 && n_layers <= 65535;
+  const auto at = [&](int l, int j) { return static_cast<const char *>(src[static_cast<int64_t>(l) * n_shards + j].data); };
+  for (int l = 2; fold && l < n_layers; ++l) {
+    fold = static_cast<char *>(dst_layers[l]) - static_cast<char *>(dst_layers[0]) ==
+           (static_cast<char *>(dst_layers[1]) - static_cast<char *>(dst_layers[0])) * l;
+    for (int j = 0; fold && j < n_shards; ++j)
+      fold = src[j].width == 0 || at(l, j) - at(0, j) == (at(1, j) - at(0, j)) * l;
+  }
+  const int64_t tiles = (rows + a.rows_per_tile - 1) / a.rows_per_tile;
+  if (tiles > INT32_MAX) return false;
+  for (int l0 = 0; l0 < n_layers; l0 += fold ? n_layers : 1) {
+    const int nl = fold ? n_layers : 1;
+    for (int j = 0; j < n_shards; ++j) {
+      a.src[j] = at(l0, j);
+      a.src_layer[j] = fold && src[j].width ? at(1, j) - at(0, j) : 0;
+    }
+    a.dst = static_cast<char *>(dst_layers[l0]);
+    a.dst_layer = fold ? static_cast<char *>(dst_layers[1]) - static_cast<char *>(dst_layers[0]) : 0;
+    head_gather_kernel<<<dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(nl)), kWideThreads, 0, stream>>>(a);
+  }
+  return true;
+}
+
 // Shape checks shared by the entry points: non-negative sizes, bytes that
 // fit int64, a device address whenever the block holds bytes.
 constexpr int64_t kMaxBytes = INT64_C(1) << 46;  // 64 TiB: no product below overflows
@@ -502,6 +610,8 @@ extern "C" int hexkv_head_concat(const hexkv_block *src, int n_layers, int n_sha
       col += b.width;
     }
   }
+  if (head_gather(src, n_layers, n_shards, dst_layers, row, static_cast<hipStream_t>(stream)))
+    return check_launch(what);
   merge_layers(moves, n_layers);
   return run_moves(moves, static_cast<hipStream_t>(stream), what);
 }

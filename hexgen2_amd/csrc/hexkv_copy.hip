@@ -25,7 +25,9 @@ namespace hexkv {
 // on the same buffers in one process (medians of 4-5 interleaved rounds):
 // 1024 x 8 21.15 ms; 512 x 8 22.2; 512 x 16 22.5; 1024 x 8 with 256 KB
 // chunks 21.4, with 64 KB 22.4; 1024 x 4 21.9; 1024 x 16 with 256 KB 21.9;
-// 512 x 4 (the earlier choice) 23.3; 256 x 8 23.6.  For reference a plain
+// 512 x 4 (the earlier choice) 23.3; 256 x 8 23.6.  Nontemporal loads and
+// stores both matter: 1024 x 8 with ordinary stores 23.3 ms, with ordinary
+// loads 21.7, against 21.1 with neither.  For reference a plain
 // chunked copy of 512 x 4 reached 5.55-5.76 TB/s (read + write), a
 // device-to-device hipMemcpy 4.90, a write-only stream 6.2-6.4 and a
 // read-only stream 7.1.

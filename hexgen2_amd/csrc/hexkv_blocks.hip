@@ -197,7 +197,9 @@ __global__ __launch_bounds__(kWideThreads) void head_gather_kernel(const GatherA
 // position Llama-3-8B prefill and 256 threads, 16 x 128 tiles moved 4.0
 // TB/s, 64 x 32 5.1, 128 x 16 5.4 and 256 x 8 5.6; 1024 threads on 512 x 8
 // tiles take 0.374 ms against 0.384 for 256 on 256 x 8 (5.74 TB/s; 512
-// threads on 256 x 8 0.398, on 512 x 8 0.376; 1024 on 1024 x 8 0.410).
+// threads on 256 x 8 0.398, on 512 x 8 0.376; 1024 on 1024 x 8 0.410, and
+// on whole-head 256 x 16 or 512 x 16 tiles, which write V in one run per
+// head, 0.403-0.406).
 constexpr int kFtRows = 512, kFtCols = 8;
 
 struct FtStoreArgs {

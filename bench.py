@@ -352,7 +352,8 @@ def cpu_baseline(w, job, budget_s):
     of append+attend, at full batch; scaled to the full workload."""
     from oracle import cpu_path
 
-    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+    # Every core this process may run on (the count is reported).
+    cores = max(1, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
     n_layers = min(2, w.layers)
     layers = [job.prefill[l].cpu() for l in range(n_layers)]
@@ -375,7 +376,7 @@ def cpu_baseline(w, job, budget_s):
         steps += 1
     layer_step = statistics.median(step_times)
     sample = (f"{n_layers} layers pack+unpack ({pu_bytes / 1e9:.2f} GB) and {steps} decode steps x 1 layer "
-              f"of append+attend, batch {w.batch}; decode scaled x{w.layers} layers")
+              f"of append+attend, batch {w.batch}; decode_ms_per_step extrapolated x{w.layers} layers")
     # The reference's own setting, one thread (hexgen2/run.py:97): one layer
     # of pack+unpack, and one decode step of one layer over the first
     # sequences of the batch (up to 8), scaled by attended positions.
@@ -392,11 +393,13 @@ def cpu_baseline(w, job, budget_s):
     scale = sum(n + 1 for n in w.lens) / sum(sub)
     single = {"value": round(2 * w.live_rows * w.row_bytes * 2 / (s1 - s0) / 1e9, 3), "unit": "GB/s", "cores": 1,
               "decode_ms_per_step": round((s3 - s2) * scale * w.layers * 1e3, 1),
+              "decode_extrapolated": True,
               "sample": f"1 layer pack+unpack; 1 decode step of 1 layer over {nb} sequences, "
-                        f"scaled x{scale:.2f} (attended positions) and x{w.layers} layers"}
+                        f"decode_ms_per_step extrapolated x{scale:.2f} (attended positions) and x{w.layers} layers"}
     torch.set_num_threads(cores)
     return {"value": round(pu_gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": sample, "decode_ms_per_step": round(layer_step * w.layers * 1e3, 1),
+            "decode_extrapolated": True, "omp_num_threads_env": os.environ.get("OMP_NUM_THREADS"),
             "pack_s": round(t1 - t0, 3), "unpack_s": round(t2 - t1, 3), "single_thread": single}
 
 
@@ -461,14 +464,16 @@ def main():
     decode_gbs = w.decode_bytes() / (decode_total_ms * 1e-3) / 1e9
     launch_bytes = w.decode_bytes() / (w.layers * w.decode_steps)
     attend_us = decode_total_ms * 1e3 / (w.layers * w.decode_steps)
-    # HBM bytes per attention launch from the hardware-counter runs (measured
-    # at decode step 0), carried to the average launch by their ratio to the
-    # algorithmic bytes of that step.
-    traffic = None
+    # HBM bytes per attention call: not measured in this run (hardware
+    # counters need a rocprofv3 --pmc run of their own).  Derived from the
+    # committed counter runs (FETCH_SIZE + WRITE_SIZE at decode step 0,
+    # calibrated on a plain copy) as their ratio to that step's algorithmic
+    # bytes, times this run's average algorithmic bytes per call.
+    traffic, traffic_ratio = None, None
     if TRAFFIC_FILE.is_file():
-        ratio = json.loads(TRAFFIC_FILE.read_text()).get(w.name, {}).get("traffic_over_algorithmic")
-        if ratio:
-            traffic = int(ratio * launch_bytes)
+        traffic_ratio = json.loads(TRAFFIC_FILE.read_text()).get(w.name, {}).get("traffic_over_algorithmic")
+        if traffic_ratio:
+            traffic = int(traffic_ratio * launch_bytes)
     result = {
         "metric": METRIC,
         "value": round(pu_gbs, 1),
@@ -491,15 +496,20 @@ def main():
         "decode_gbs": round(decode_gbs, 1),
         "decode_hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": f"attend_{job.kernel_name}_kernel + combine_kernel (fused append+attend, one layer)",
+            "kernel": f"one hexkv_attend call = attend_{job.kernel_name}_kernel + combine_kernel "
+                      "(fused append+attend, one layer)",
             "bound": "hbm",
             "achieved": round(launch_bytes / (attend_us * 1e-6) / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(launch_bytes / (attend_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": (f"derived: committed PMC ratio {traffic_ratio} (profiles/traffic.json, decode "
+                               "step 0) x this run's algorithmic bytes per call") if traffic else None,
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_us": round(attend_us, 2),
+            "timing": "HIP events on the launch stream around every timed decode step; avg_launch_us = "
+                      "decode time / (layers x steps), i.e. the attention kernel plus its combine kernel",
         },
         "cpu_baseline": None,
     }

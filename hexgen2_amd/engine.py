@@ -85,7 +85,10 @@ class Engine:
         return logits.argmax(-1), cache, logits
 
     @torch.inference_mode()
-    def decode(self, first_token, cache, prompt_length, max_new_tokens, on_token=None):
+    def decode(self, first_token, cache, prompt_length, max_new_tokens, on_token=None, *, on_logits=None):
+        """Greedy decode from the handed-off cache (model.py:86-120).
+        ``on_logits`` (an addition) receives each decode step's logits
+        ``[1, vocab]``, for logit-level checks."""
         token = first_token.to(self.device).reshape(1)
         generated = [int(token.item())]
         if on_token:
@@ -112,6 +115,8 @@ class Engine:
             logits = self.model.forward(token[:, None], inference_params=state, last_token_only=True,
                                         fused_append=self.fused_append)
             state.sequence_len_offset += 1
+            if on_logits:
+                on_logits(logits)
             token = logits.argmax(-1)
             generated.append(int(token.item()))
             if on_token:

@@ -22,7 +22,9 @@ class InferenceParams:
     pack], V [B, H, S, D])``; ``sequence_len_offset`` is the number of
     positions already cached (the append position of the next token);
     ``lengths_per_sample`` (int32, device), when set, gives each sequence's
-    own position on the FT path.
+    own position (its cached length) in a ragged decode batch, on the FT path
+    and on the standard layout alike; ``sequence_len_offset`` then bounds
+    every sample's position.
     """
     max_sequence_len: int
     max_batch_size: int = 1

@@ -114,8 +114,17 @@ class LlamaHost:
             state.update(values)
         return cls(shape, state, device, dtype)
 
-    def _rope(self, x: torch.Tensor, offset: int) -> torch.Tensor:
+    def _rope(self, x: torch.Tensor, offset: int, positions=None) -> torch.Tensor:
+        """Rotary (GPT-NeoX halves) of ``x [B, S, H, D]`` at positions
+        ``offset + s``, or for one new token per sequence (S == 1) at each
+        sequence's own ``positions[b]`` (a ragged decode batch)."""
         seqlen = x.shape[1]
+        if positions is not None:
+            freqs = positions.to(torch.float32)[:, None] * self.inv_freq[None, :]  # [B, D/2]
+            emb = torch.cat((freqs, freqs), dim=-1)
+            cos = emb.cos().to(x.dtype)[:, None, None, :]
+            sin = emb.sin().to(x.dtype)[:, None, None, :]
+            return x * cos + _rotate_half(x) * sin
         pos = torch.arange(offset, offset + seqlen, device=self.device, dtype=torch.float32)
         freqs = torch.outer(pos, self.inv_freq)
         emb = torch.cat((freqs, freqs), dim=-1)
@@ -130,6 +139,12 @@ class LlamaHost:
         batch, seqlen = input_ids.shape
         d = s.head_dim
         offset = inference_params.sequence_len_offset
+        # A ragged decode batch: each sequence's token sits at its own cached
+        # length (lengths_per_sample, generation.py:30).
+        positions = None
+        if inference_params.lengths_per_sample is not None and seqlen == 1 and offset > 0:
+            b0 = inference_params.batch_size_offset
+            positions = inference_params.lengths_per_sample[b0:b0 + batch]
         h = F.embedding(input_ids, self.embed)
         for i, layer in enumerate(self.layers):
             x = rms_norm(h, layer["ln1"], s.rms_norm_eps)
@@ -141,7 +156,7 @@ class LlamaHost:
                 context = _apply_rotary_single_query_attention(q, inference_params, i, d, s.rope_theta,
                                                                kv=torch.stack((k, v), dim=2))
             else:
-                q, k = self._rope(q, offset), self._rope(k, offset)
+                q, k = self._rope(q, offset, positions), self._rope(k, offset, positions)
                 kv = torch.stack((k, v), dim=2)  # [B, S, 2, Hkv, D]
                 if fused_append and offset > 0 and seqlen == 1 and i in inference_params.key_value_memory_dict:
                     context = update_and_attend(q, kv, inference_params, i, self.scale)

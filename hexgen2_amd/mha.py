@@ -37,11 +37,45 @@ def allocate_inference_cache(batch_size: int, max_seqlen: int, num_heads_kv: int
     return (torch.empty(k_shape, dtype=dtype, device=device), torch.empty(v_shape, dtype=dtype, device=device))
 
 
+# Attribute of the cache view _update_kv_cache returns for a ragged decode
+# step: (seqlens, bias) with sequence b attending seqlens[b] + bias keys.
+_SEQLENS_ATTR = "_hexkv_seqlens"
+
+
+def _sample_positions(inference_params, batch_start: int, batch_end: int) -> Optional[torch.Tensor]:
+    """``lengths_per_sample[batch_start:batch_end]`` as a contiguous int32
+    device tensor (each sequence's cached length, i.e. the position its next
+    token is written at), or None when the batch shares
+    ``sequence_len_offset``.  ``lengths_per_sample`` is the field the
+    reference reads per-sample positions from (generation.py:30, used at
+    mha.py:327-328)."""
+    lengths = inference_params.lengths_per_sample
+    if lengths is None:
+        return None
+    if lengths.dim() != 1 or lengths.shape[0] < batch_end:
+        raise ValueError(f"lengths_per_sample of shape {tuple(lengths.shape)} does not cover "
+                         f"sequences [{batch_start}, {batch_end})")
+    positions = lengths[batch_start:batch_end]
+    if positions.dtype != torch.int32 or not positions.is_contiguous():
+        positions = positions.to(torch.int32).contiguous()
+    return positions
+
+
 def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torch.Tensor:
     """kv: (batch, seqlen, 2, kv_heads, head_dim).  Writes kv at
     ``[batch_size_offset:+batch, sequence_len_offset:+seqlen]`` of layer
     ``layer_idx``'s cache (allocated on first use) and returns the view
-    ``cache[batch_start:batch_end, :sequence_end]`` (mha.py:255-288)."""
+    ``cache[batch_start:batch_end, :sequence_end]`` (mha.py:255-288).
+
+    Ragged decode: when ``inference_params.lengths_per_sample`` is set and
+    seqlen is 1, sequence b's row is written at ``lengths_per_sample[b]``
+    instead (the reference keeps one offset for the whole batch,
+    mha.py:276-279, and reads per-sample positions only on the FT path,
+    mha.py:327-328).  ``sequence_len_offset`` must then bound every sample's
+    position (the returned view spans ``sequence_len_offset + 1`` positions),
+    and the view carries the per-sample key counts so that
+    ``FlashCrossAttention`` attends ``lengths_per_sample[b] + 1`` keys of
+    row b rather than the whole view."""
     if inference_params.fused_ft_kernel:
         return _update_ft_cache(kv, inference_params, layer_idx)
     num_heads, head_dim = kv.shape[-2:]
@@ -59,13 +93,19 @@ def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torc
     assert sequence_end <= cache.shape[1]
     kv = kv.contiguous()
     target = cache[batch_start:batch_end]
-    if kv.shape[1] == 1:
+    positions = _sample_positions(inference_params, batch_start, batch_end) if kv.shape[1] == 1 else None
+    if positions is not None:
+        ops.append_kv(target, kv.reshape(kv.shape[0], -1), positions)
+    elif kv.shape[1] == 1:
         ops.append_kv(target, kv.reshape(kv.shape[0], -1), position_bias=sequence_start)
     elif kv.shape[1] > 1:
         # A multi-position write (prefill) is an unpack of one packed layer with
         # uniform lengths into the cache shifted by sequence_start rows.
         ops.unpack_live([kv.reshape(-1)], [target[:, sequence_start:]], [kv.shape[1]] * kv.shape[0])
-    return cache[batch_start:batch_end, :sequence_end]
+    view = cache[batch_start:batch_end, :sequence_end]
+    if positions is not None:
+        setattr(view, _SEQLENS_ATTR, (positions, 1))
+    return view
 
 
 def _update_ft_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torch.Tensor:
@@ -147,7 +187,13 @@ class FlashCrossAttention(nn.Module):
         self.drop = nn.Dropout(attention_dropout)
 
     def forward(self, q, kv, causal=None, cu_seqlens=None, max_seqlen=None,
-                cu_seqlens_k=None, max_seqlen_k=None):
+                cu_seqlens_k=None, max_seqlen_k=None, *, seqlens_k=None):
+        """``seqlens_k`` (device int32 ``[B]``, an addition to the reference
+        signature) makes row b attend only its first ``seqlens_k[b]`` keys of
+        the ``Sk`` in ``kv`` (a ragged decode batch in a padded cache).  A
+        view returned by ``_update_kv_cache`` for a ragged step carries these
+        counts itself, so the reference's call ``inner_cross_attn(q, kv,
+        causal=False)`` (mha.py:568-569) needs no change."""
         assert q.dtype in (torch.float16, torch.bfloat16, torch.float32)
         assert q.is_cuda and kv.is_cuda
         if cu_seqlens is not None or cu_seqlens_k is not None:
@@ -156,10 +202,19 @@ class FlashCrossAttention(nn.Module):
         batch_size = q.shape[0]
         seqlen_k = kv.shape[1]
         assert kv.shape[0] == batch_size and kv.shape[4] == q.shape[3]
+        bias = seqlen_k
+        if seqlens_k is None and getattr(kv, _SEQLENS_ATTR, None) is not None:
+            seqlens_k, bias = getattr(kv, _SEQLENS_ATTR)
+            bias = int(bias)
+        elif seqlens_k is not None:
+            bias = 0
+        if seqlens_k is not None:
+            assert seqlens_k.dtype == torch.int32 and seqlens_k.is_cuda and seqlens_k.numel() == batch_size
+            seqlens_k = seqlens_k.contiguous()
         q = q if q.stride(-1) == 1 and q.stride(-2) == q.shape[-1] else q.contiguous()
         if kv.stride(-1) != 1 or kv.stride(-2) != kv.shape[-1] or kv.stride(1) != kv[0, 0].numel():
             kv = kv.contiguous()
-        return ops.decode_attention(q, kv, max_seqlen=seqlen_k, seqlen_bias=seqlen_k,
+        return ops.decode_attention(q, kv, max_seqlen=seqlen_k, seqlens=seqlens_k, seqlen_bias=bias,
                                     causal=bool(causal) and q.shape[1] > 1,
                                     softmax_scale=self.softmax_scale)
 
@@ -169,7 +224,9 @@ def update_and_attend(q: torch.Tensor, kv: torch.Tensor, inference_params, layer
     """The decode-step pair ``_update_kv_cache`` + ``inner_cross_attn(q, kv,
     causal=False)`` (mha.py:565-569) as one fused HIP launch: the new row is
     written to the cache and attended from registers.  q (B, 1, H, D),
-    kv (B, 1, 2, H_k, D)."""
+    kv (B, 1, 2, H_k, D).  With ``lengths_per_sample`` set, row b is written
+    at ``lengths_per_sample[b]`` and attends that many keys plus the new one;
+    ``sequence_len_offset`` bounds every sample's position."""
     cache = inference_params.key_value_memory_dict[layer_idx]
     batch_start = inference_params.batch_size_offset
     batch_end = batch_start + kv.shape[0]
@@ -177,5 +234,7 @@ def update_and_attend(q: torch.Tensor, kv: torch.Tensor, inference_params, layer
     assert kv.shape[1] == 1 and q.shape[1] == 1
     assert batch_end <= cache.shape[0] and offset + 1 <= cache.shape[1]
     target = cache[batch_start:batch_end]
-    return ops.decode_attention(q.contiguous(), target, max_seqlen=offset + 1, seqlen_bias=offset,
+    positions = _sample_positions(inference_params, batch_start, batch_end)
+    return ops.decode_attention(q.contiguous(), target, max_seqlen=offset + 1, seqlens=positions,
+                                seqlen_bias=0 if positions is not None else offset,
                                 kv_new=kv.contiguous(), softmax_scale=softmax_scale)

@@ -413,15 +413,45 @@ def ft_attend(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache
     return out
 
 
+def _tensor_geometry(t: Optional[torch.Tensor]):
+    """Everything about a tensor a prebuilt parameter block depends on apart
+    from its address: shape, strides, dtype, device and contiguity."""
+    if t is None:
+        return None
+    return tuple(t.shape), t.stride(), t.dtype, t.device, t.is_contiguous()
+
+
+def _plan_geometry(q, cache, out, kv_new) -> tuple:
+    """The key an ``AttendPlan`` compares per call: the geometry of q, cache,
+    out and kv_new (None when the call has no fused append)."""
+    return tuple(_tensor_geometry(t) for t in (q, cache, out, kv_new))
+
+
+def _check_plan_geometry(want: tuple, got: tuple) -> None:
+    """Raise ValueError naming the first tensor whose geometry differs from
+    the plan's."""
+    if want == got:
+        return
+    for name, a, b in zip(("q", "cache", "out", "kv_new"), want, got):
+        if a != b:
+            if a is None or b is None:
+                raise ValueError("AttendPlan built with kv_new must be called with kv_new, and only then")
+            raise ValueError(f"AttendPlan called with a different {name} geometry: "
+                             f"built for shape/strides/dtype/device/contiguous {a}, got {b}")
+
+
 class AttendPlan:
     """Prebuilt ``hexkv_attend`` parameters for a decode loop on one geometry.
 
     Building the parameter block once and patching only pointers, the length
     bias and ``max_seqlen`` per call keeps host overhead per layer small; the
     workspace is allocated once for the largest ``max_seqlen`` the loop will
-    use.  Each call launches on the current stream (so a call inside
-    ``torch.cuda.graph`` capture is recorded into the graph).  Arguments as
-    for ``decode_attention``; a plan built with ``kv_new`` is called with one.
+    use.  Every call checks that q, cache, out and kv_new have exactly the
+    geometry (shape, strides, dtype, device) the block was built for, since
+    only their addresses are patched.  Each call launches on the current
+    stream (so a call inside ``torch.cuda.graph`` capture is recorded into
+    the graph).  Arguments as for ``decode_attention``; a plan built with
+    ``kv_new`` is called with one.
     """
 
     def __init__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *,
@@ -440,15 +470,16 @@ class AttendPlan:
         self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), self.workspace.numel()
         self.device = q.device
         self.fused = kv_new is not None
-        self.shapes = (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype)
+        self.geometry = _plan_geometry(q, cache, out, kv_new)
+
+    def check(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
+              kv_new: Optional[torch.Tensor]) -> None:
+        """Raise ValueError unless the tensors match the plan's geometry."""
+        _check_plan_geometry(self.geometry, _plan_geometry(q, cache, out, kv_new))
 
     def __call__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
                  kv_new: Optional[torch.Tensor], seqlen_bias: int, max_seqlen: int) -> torch.Tensor:
-        if (tuple(q.shape), tuple(cache.shape), cache.stride(), q.dtype) != self.shapes \
-                or tuple(out.shape) != self.shapes[0] or out.dtype != q.dtype:
-            raise ValueError("AttendPlan called with a different geometry")
-        if (kv_new is not None) != self.fused:
-            raise ValueError("AttendPlan built with kv_new must be called with kv_new, and only then")
+        self.check(q, cache, out, kv_new)
         p = self.params
         p.q, p.cache, p.out = q.data_ptr(), cache.data_ptr(), out.data_ptr()
         if kv_new is not None:
@@ -492,6 +523,9 @@ class DecodeStepGraph:
         self.plan = AttendPlan(self.q[0], self.cache[0], self.out[0], max_seqlens=[self.max_seqlen],
                                seqlens=positions, kv_new=self.kv_new[0], softmax_scale=softmax_scale,
                                kernel=kernel)
+        # Every layer is checked before anything is captured.
+        for l in range(len(self.q)):
+            self.plan.check(self.q[l], self.cache[l], self.out[l], self.kv_new[l])
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             for l in range(len(self.q)):

@@ -9,6 +9,12 @@
   full-context recompute.
 * Transferred-cache tokens must equal the colocated run (hexgen2/run.py:
   167-176 semantics), with and without the fused append+attend.
+* Logits: the reference validator accepts a run when its prefill logits
+  satisfy ``torch.allclose(logits, hf_logits, atol=0.03, rtol=0.03)`` against
+  HuggingFace eager in the same dtype (hexgen2/validate.py:33-43).  Here
+  that bar holds at prefill and at every decode step, for every prompt the
+  engine decodes (tests/golden/hf_logits.json, make_logits.py); float32
+  logits must also agree with HuggingFace float32 within 1e-4.
 """
 import json
 from pathlib import Path
@@ -23,19 +29,44 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 GREEDY = json.loads((GOLDEN / "greedy.json").read_text())
+HF_LOGITS = json.loads((GOLDEN / "hf_logits.json").read_text())["models"]
+
+
+def hf_logits(model, prompt, dtype):
+    """HuggingFace's per-step logits for this prompt, [steps, vocab]."""
+    for case in HF_LOGITS[model]:
+        if case["prompt"] == list(prompt):
+            return torch.tensor(case["logits"][dtype]), torch.tensor(case["logits"]["float32"])
+    raise KeyError(f"no golden logits for {model} prompt {prompt}")
+
+
+def check_logits(model, prompt, dtype, logits):
+    """validate.py:43's bar at every step against HF in the same dtype; fp32
+    also within 1e-4 of HF fp32."""
+    want, want32 = hf_logits(model, prompt, dtype)
+    got = torch.stack([x.reshape(-1).float().cpu() for x in logits])
+    assert got.shape == want.shape, (got.shape, want.shape)
+    for i in range(len(got)):
+        assert torch.allclose(got[i], want[i], atol=0.03, rtol=0.03), \
+            f"step {i}: max logit error {float((got[i] - want[i]).abs().max())}"
+    if dtype == "float32":
+        err = float((got - want32).abs().max())
+        assert err <= 1e-4, f"float32 logits differ from HF float32 by {err}"
 
 
 def run_split(engine, prompt, count):
-    """Prefill, hand the cache over a same-GPU channel, decode (run.py:141-198)."""
+    """Prefill, hand the cache over a same-GPU channel, decode (run.py:141-198).
+    Returns (tokens, packet bytes, per-step logits)."""
     prefill_side, decode_side = DeviceChannel.pair()
-    first, cache, _ = engine.prefill(prompt, count)
+    first, cache, logits = engine.prefill(prompt, count)
+    steps = [logits]
     sent = send_packet({"first": first, **{str(k): v for k, v in cache.items()}},
                        {"id": "r", "prompt_length": len(prompt)}, dst=1, channel=prefill_side)
     tensors, metadata = recv_packet(src=0, channel=decode_side)
     assert metadata == {"id": "r", "prompt_length": len(prompt)}
     tokens = engine.decode(tensors["first"], {int(k): v for k, v in tensors.items() if k != "first"},
-                           len(prompt), count)
-    return tokens, sent
+                           len(prompt), count, on_logits=steps.append)
+    return tokens, sent, steps
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
@@ -43,19 +74,44 @@ def test_fixture_tokens_match_reference_gpu_run(device, dtype):
     engine = Engine(GOLDEN / "fixture_seed17", "native", "cuda", dtype)
     for case in GREEDY["fixture_seed17"]:
         print(f"fixture {dtype} prompt={case['prompt']}", flush=True)
-        tokens, sent = run_split(engine, case["prompt"], case["max_new_tokens"])
+        tokens, sent, logits = run_split(engine, case["prompt"], case["max_new_tokens"])
         assert tokens == case["reference_gpu_fp16_tokens"] == case["hf_fp32_tokens"]
         elem = 4 if dtype == "float32" else 2
         # int64 first token + 2 layers x L x (2 x 2 heads x 32 dims) live bytes
         assert sent == 8 + 2 * len(case["prompt"]) * 2 * 2 * 32 * elem
+        check_logits("fixture_seed17", case["prompt"], dtype, logits)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("fused", [False, True])
+def test_trace_prompts_tokens_and_logits(device, dtype, fused):
+    # the pilot trace's requests (configs/tiny-trace.jsonl) on the fixture
+    trace = json.loads((GOLDEN / "trace_tokens.json").read_text())
+    requests = [json.loads(s) for s in (GOLDEN / "tiny-trace.jsonl").read_text().splitlines() if s.strip()]
+    engine = Engine(GOLDEN / "fixture_seed17", "native", "cuda", dtype, fused_append=fused)
+    for row in requests:
+        print(f"trace {row['id']} {dtype} fused={fused}", flush=True)
+        tokens, _, logits = run_split(engine, row["input_ids"], row["max_new_tokens"])
+        assert tokens == trace[row["id"]]["hf_fp32_tokens"]
+        check_logits("fixture_seed17", row["input_ids"], dtype, logits)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_tiny_llama_16bit_tokens_and_logits(device, dtype):
+    case = GREEDY["tiny_llama"][0]
+    engine = Engine(GOLDEN / "tiny_llama", "native", "cuda", dtype)
+    tokens, _, logits = run_split(engine, case["prompt"], case["max_new_tokens"])
+    assert tokens == case["hf_fp32_tokens"]
+    check_logits("tiny_llama", case["prompt"], dtype, logits)
 
 
 @pytest.mark.parametrize("fused", [False, True])
 def test_tiny_llama_fp32_golden_and_colocated(device, fused):
     case = GREEDY["tiny_llama"][0]
     engine = Engine(GOLDEN / "tiny_llama", "native", "cuda", "float32", fused_append=fused)
-    tokens, sent = run_split(engine, case["prompt"], case["max_new_tokens"])
+    tokens, sent, logits = run_split(engine, case["prompt"], case["max_new_tokens"])
     assert tokens == case["hf_fp32_tokens"]
+    check_logits("tiny_llama", case["prompt"], "float32", logits)
     assert sent == 8 + 2 * 16 * (2 * 4 * 16 * 4)
     # colocated: same engine, no transfer (run.py:168-169)
     first, cache, _ = engine.prefill(case["prompt"], case["max_new_tokens"])
@@ -83,18 +139,22 @@ def test_prefill_cache_is_one_packed_buffer(device):
     assert int(first) == int(logits.argmax(-1))
 
 
-def greedy_ft(host, prompt, count):
+def greedy_ft(host, prompt, count, steps=None):
     """The reference's fused_ft_kernel decode (generation.py:77-140 with
     fused_ft_kernel=True): prefill writes the FT caches, every decode step
-    rotates, appends and attends in one FT call."""
+    rotates, appends and attends in one FT call.  ``steps`` collects each
+    step's logits."""
     from hexgen2_amd.generation import InferenceParams
+    steps = [] if steps is None else steps
     params = InferenceParams(max_sequence_len=len(prompt) + count, max_batch_size=1, fused_ft_kernel=True)
     logits = host.forward(torch.tensor([prompt], device="cuda"), params)
+    steps.append(logits)
     token = int(logits.argmax(-1))
     tokens = [token]
     params.sequence_len_offset = len(prompt)
     for _ in range(count - 1):
         logits = host.forward(torch.tensor([[token]], device="cuda"), params)
+        steps.append(logits)
         token = int(logits.argmax(-1))
         tokens.append(token)
         params.sequence_len_offset += 1
@@ -108,7 +168,9 @@ def test_ft_decode_tokens_match_reference(device, dtype):
     host = LlamaHost.load(GOLDEN / "fixture_seed17", "cuda", getattr(torch, dtype))
     for case in GREEDY["fixture_seed17"]:
         print(f"ft fixture {dtype} prompt={case['prompt']}", flush=True)
-        assert greedy_ft(host, case["prompt"], case["max_new_tokens"]) == case["reference_gpu_fp16_tokens"]
+        steps = []
+        assert greedy_ft(host, case["prompt"], case["max_new_tokens"], steps) == case["reference_gpu_fp16_tokens"]
+        check_logits("fixture_seed17", case["prompt"], dtype, steps)
     if dtype == "float32":
         tiny = LlamaHost.load(GOLDEN / "tiny_llama", "cuda", torch.float32)
         case = GREEDY["tiny_llama"][0]

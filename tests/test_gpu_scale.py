@@ -1,0 +1,118 @@
+"""Parity at the measured configurations' real sizes.
+
+Decode attention with the fused append (one layer, one decode step) for the
+four GPU workloads at their seeded ragged lengths, against the float64
+oracle: TinyLlama-1.1B (1 x 512 positions, fp16), Llama-2-7B (8 rows of
+U[256, 2048], fp16), the Llama-2-70B TP-8 share (32 rows of U[512, 4096],
+bf16, one KV head per 8 query heads) and Llama-3-8B (64 rows of U[128, 8192],
+bf16), each at the first and at the last decode step, where the longest
+rows reach the cache capacity (8153 positions in the seeded Llama-3-8B draw:
+16 partitions of 512).  Both score kernels run every case with the library's
+partition choice, and again with 128-position partitions (up to 64 per row:
+the combine kernel's deep register path).  The append is checked bit-exactly
+against the oracle over
+the whole layer (the new row at each sequence's position, every other byte
+unchanged); attention within 2e-3 (fp16) / 8e-3 (bf16) max-abs.
+
+The full Llama-3-8B handoff -- pack of all 32 layers' live rows (243,613
+rows of 4 KB per layer, 31.9 GB) and unpack into a sentinel-filled decode
+cache -- is checked on the device through size-independent properties: the
+packed buffer is the live rows in batch order, the unpacked live rows equal
+the prefill cache's, and every row past a sequence's length still holds the
+sentinel (hexgen2/model.py:81, :101-108).
+"""
+import numpy as np
+import pytest
+import torch
+
+from hexgen2_amd import ops
+from hexgen2_amd.workloads import workload
+from oracle import kv_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 8e-3}
+
+
+def bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy()
+
+
+def attend_oracle(q, cache, lens):
+    """float64 oracle, one sequence at a time (bounded host memory)."""
+    out = np.zeros(q.shape, dtype=np.float64)
+    qd = q.detach().cpu().double().numpy()
+    for b, n in enumerate(lens):
+        kv = cache[b, :n].detach().cpu().double().numpy()[None]
+        out[b:b + 1] = oracle.attend(qd[b:b + 1], kv, [n])
+    return out
+
+
+CASES = [("tinyllama-1.1b", 0), ("tinyllama-1.1b", 127), ("llama2-7b", 0), ("llama2-7b", 63),
+         ("llama2-70b-tp8", 0), ("llama2-70b-tp8", 31), ("llama3-8b", 0), ("llama3-8b", 255)]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name,step", CASES)
+def test_decode_step_at_full_size(device, name, step):
+    w = workload(name)
+    B, cap = w.batch, w.capacity
+    pos = [n + step for n in w.lens]  # cached rows before this step; the new row lands here
+    print(f"{name} step {step}: batch {B}, capacity {cap}, longest row {max(pos) + 1}", flush=True)
+    g = torch.Generator(device=device).manual_seed(w.seed + 100 + step)
+    base = torch.empty((B, cap, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=device).normal_(generator=g)
+    q = torch.empty((B, 1, w.q_heads, w.head_dim), dtype=w.dtype, device=device).normal_(generator=g)
+    kv_new = torch.empty((B, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=device).normal_(generator=g)
+    seqlens = torch.tensor(pos, dtype=torch.int32, device=device)
+    want_cache = oracle.append(bits(base), bits(kv_new), pos)
+    outs = {}
+    for kernel in ("valu", "mfma"):
+        for partition in (0, 128):
+            cache = base.clone()
+            outs[kernel, partition] = ops.decode_attention(q, cache, max_seqlen=max(pos) + 1, seqlens=seqlens,
+                                                           kv_new=kv_new, kernel=kernel, partition=partition)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(cache), want_cache), f"{kernel}/{partition}: fused append differs"
+            print(f"  {kernel} partition {partition or 'auto'}: append bit-exact", flush=True)
+            del cache
+    after = base.clone()
+    ops.append_kv(after, kv_new.reshape(B, -1), seqlens)
+    ref = attend_oracle(q, after, [n + 1 for n in pos])
+    for kernel, out in outs.items():
+        err = float(np.abs(out.cpu().double().numpy() - ref).max())
+        print(f"  {kernel}: attention max-abs {err:.2e}", flush=True)
+        assert err <= TOL[w.dtype], f"{kernel}: max-abs {err} above {TOL[w.dtype]}"
+    del base, after
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(600)
+def test_llama3_8b_full_handoff_round_trip(device):
+    w = workload("llama3-8b")
+    L, B, cap = w.layers, w.batch, w.capacity
+    shape = (L, B, cap, 2, w.kv_heads, w.head_dim)
+    print(f"full handoff: {L} layers x {w.live_rows} live rows of {w.row_bytes} B", flush=True)
+    g = torch.Generator(device=device).manual_seed(w.seed + 1)
+    prefill = torch.empty(shape, dtype=w.dtype, device=device)
+    for l in range(L):
+        prefill[l].normal_(generator=g)
+    sentinel = 0x7FC1  # a bf16 NaN pattern: no normal draw produces it
+    decode = torch.empty(shape, dtype=w.dtype, device=device)
+    decode.view(torch.int16).fill_(sentinel)
+    packed = ops.pack_live(prefill, w.lens)
+    ops.unpack_live(packed, decode, w.lens)
+    torch.cuda.synchronize()
+    print("  pack + unpack done", flush=True)
+    assert tuple(packed.shape) == (L, w.live_rows, 2, w.kv_heads, w.head_dim)
+    pi, di, ki = prefill.view(torch.int16), decode.view(torch.int16), packed.view(torch.int16)
+    start = 0
+    for b, n in enumerate(w.lens):
+        live = pi[:, b, :n]
+        assert torch.equal(ki[:, start:start + n], live), f"packed rows of sequence {b}"
+        assert torch.equal(di[:, b, :n], live), f"unpacked rows of sequence {b}"
+        assert bool((di[:, b, n:] == sentinel).all()), f"rows past the length of sequence {b} changed"
+        start += n
+    assert start == w.live_rows
+    print("  round trip bit-exact, padding untouched", flush=True)
+    del prefill, decode, packed, pi, di, ki
+    torch.cuda.empty_cache()

@@ -25,38 +25,57 @@ def fixture_cache(dtype):
             2: torch.full((1, 3, 2, 1, 4), -1.25, dtype=dtype)}
 
 
-def _worker(rank, rendezvous):
+def _echo_peer(rank, rendezvous, failures):
+    """Two processes over Gloo: rank 0 sends each dtype's fixture
+    (send_data), rank 1 receives it and sends back exactly what it got, rank
+    0 receives the echo.  Both sides check what they received against the
+    fixture bit for bit; then one send_packet/recv_packet with an empty
+    tensor and metadata.  Failures go to the parent through ``failures``."""
     torch.set_num_threads(1)
     dist.init_process_group("gloo", rank=rank, world_size=2, init_method=Path(rendezvous).as_uri(),
                             timeout=timedelta(seconds=30))
+    peer = 1 - rank
+    token = torch.tensor([42, 17], dtype=torch.long)
     try:
         for dtype in (torch.float16, torch.bfloat16, torch.float32):
             cache = fixture_cache(dtype)
-            token = torch.tensor([42, 17], dtype=torch.long)
-            if rank == 0:
-                send_data(token, cache, dst=1)
-                received, returned = recv_data(src=1, num_layers=2)
+            if rank == 1:  # echo side: receive, then return what arrived
+                got_token, got_cache = recv_data(src=peer, num_layers=len(cache))
+                send_data(got_token, got_cache, dst=peer)
             else:
-                received, returned = recv_data(src=0, num_layers=2)
-                send_data(received, returned, dst=0)
-            torch.testing.assert_close(received, token, rtol=0, atol=0)
-            if list(returned) != [7, 2]:
-                raise AssertionError("Layer IDs/order changed")
-            for key in cache:
-                torch.testing.assert_close(returned[key], cache[key], rtol=0, atol=0)
-        # a packet with an empty tensor and metadata survives too
+                send_data(token, cache, dst=peer)
+                got_token, got_cache = recv_data(src=peer, num_layers=len(cache))
+            assert list(got_cache) == [7, 2], f"{dtype}: layer order {list(got_cache)}"
+            assert torch.equal(got_token, token), f"{dtype}: token {got_token}"
+            for layer, want in cache.items():
+                assert got_cache[layer].dtype == want.dtype and torch.equal(got_cache[layer], want), \
+                    f"{dtype}: layer {layer} changed on the wire"
         if rank == 0:
-            send_packet({"a": torch.zeros((0, 3)), "b": torch.tensor([1.5])}, {"id": "r1"}, dst=1)
+            send_packet({"a": torch.zeros((0, 3)), "b": torch.tensor([1.5])}, {"id": "r1"}, dst=peer)
         else:
-            tensors, meta = recv_packet(src=0)
-            assert meta == {"id": "r1"} and tensors["a"].shape == (0, 3)
-            torch.testing.assert_close(tensors["b"], torch.tensor([1.5]), rtol=0, atol=0)
+            tensors, meta = recv_packet(src=peer)
+            assert meta == {"id": "r1"} and tuple(tensors["a"].shape) == (0, 3)
+            assert torch.equal(tensors["b"], torch.tensor([1.5]))
+    except Exception as error:  # reported by the parent with the rank that saw it
+        failures.put((rank, repr(error)))
+        raise
     finally:
         dist.destroy_process_group()
 
 
 def test_lossless_real_process_roundtrip(tmp_path):
-    mp.spawn(_worker, args=(str(tmp_path / "rendezvous"),), nprocs=2, join=True)
+    ctx = mp.get_context("spawn")
+    failures = ctx.SimpleQueue()
+    procs = [ctx.Process(target=_echo_peer, args=(r, str(tmp_path / "rendezvous"), failures)) for r in (0, 1)]
+    for p in procs:
+        p.start()
+    for p in procs:
+        p.join(120)
+    seen = []
+    while not failures.empty():
+        seen.append(failures.get())
+    assert not seen, seen
+    assert [p.exitcode for p in procs] == [0, 0]
 
 
 @pytest.mark.parametrize("shape", [[-1], [True], [2 ** 40], [1] * 9])

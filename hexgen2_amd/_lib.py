@@ -21,7 +21,9 @@ MAX_SEQS_PER_LAUNCH = 256
 EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "hexkv_append",
            "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
-           "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend")
+           "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend",
+           "hexkv_attend_noalloc")
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
 class AttendParams(ctypes.Structure):
@@ -100,6 +102,8 @@ def load() -> ctypes.CDLL:
     lib.hexkv_attend_kernel.argtypes = [ctypes.POINTER(AttendParams)]
     lib.hexkv_attend.restype = ci
     lib.hexkv_attend.argtypes = [ctypes.POINTER(AttendParams), vp, ctypes.c_size_t, vp]
+    lib.hexkv_attend_noalloc.restype = ci
+    lib.hexkv_attend_noalloc.argtypes = [ctypes.POINTER(AttendParams), vp]
     blocks = ctypes.POINTER(Block)
     lib.hexkv_flat_concat.restype = ci
     lib.hexkv_flat_concat.argtypes = [blocks, ci, vp, vp]

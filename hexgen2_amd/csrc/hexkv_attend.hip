@@ -47,6 +47,8 @@
 #include "hexkv_common.h"
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 namespace hexkv {
 
@@ -1197,10 +1199,12 @@ extern "C" int hexkv_attend_kernel(const hexkv_attend_params *p) {
   return use_mfma(p, kernel_group(p->q_heads / p->kv_heads)) ? HEXKV_KERNEL_MFMA : HEXKV_KERNEL_VALU;
 }
 
-extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_t ws_bytes,
-                            hexkv_stream_t stream) {
-  using namespace hexkv;
-  clear_error();
+namespace hexkv {
+
+// The launch behind hexkv_attend and hexkv_attend_noalloc: validated
+// parameters, a workspace of ws_bytes bytes (device memory), one stream.
+static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t ws_bytes,
+                         hexkv_stream_t stream, const char *what) {
   int rc = validate(p);
   if (rc != HEXKV_OK || p->batch == 0) return rc;
   const int part = choose_partition(p);
@@ -1208,10 +1212,9 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
   const int64_t max_parts = max_parts_of(p, part);
   const size_t need = workspace_bytes(p, part);
   if (need > 0 && (!workspace || ws_bytes < need))
-    return fail(HEXKV_EWORKSPACE, "hexkv_attend: workspace of %zu bytes needed, %zu given", need,
-                ws_bytes);
+    return fail(HEXKV_EWORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, need, ws_bytes);
   if (need > 0 && !aligned16(workspace))
-    return fail(HEXKV_EINVAL, "hexkv_attend: workspace must be 16-byte aligned");
+    return fail(HEXKV_EINVAL, "%s: workspace must be 16-byte aligned", what);
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
 
   AttendArgs a{};
@@ -1260,7 +1263,76 @@ extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_
     default: rc = dispatch_d<float>(p->head_dim, G, a, grid, kind, s); break;
   }
   if (rc != HEXKV_OK) return rc;
-  return check_launch("hexkv_attend");
+  return check_launch(what);
+}
+
+// hexkv_attend_noalloc's workspace: one array per GPU the library runs on,
+// held until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address); it
+// uses the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[HEXKV_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<void *> g_scratch_addr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the device that runs `stream` (the current
+// device for the null stream), looked up once per device with that device
+// current.
+static int scratch_address(hexkv_stream_t stream, void **addr, const char *what) {
+  int dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: cannot tell the stream's device: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(HEXKV_EUNSUPPORTED, "%s: device %d beyond the %d the library tracks", what, dev, kMaxScratchDevices);
+  void *ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (ptr) {
+    *addr = ptr;
+    return HEXKV_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ptr = g_scratch_addr[dev].load(std::memory_order_relaxed);
+  if (!ptr) {
+    int current = 0;
+    e = hipGetDevice(&current);
+    if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+    if (current != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(HEXKV_EHIP, "%s: hipSetDevice(%d): %s", what, dev, hipGetErrorString(e));
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t back = current != dev ? hipSetDevice(current) : hipSuccess;
+    if (e != hipSuccess || !ptr)
+      return fail(HEXKV_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev, hipGetErrorString(e));
+    if (back != hipSuccess)
+      return fail(HEXKV_EHIP, "%s: restoring device %d: %s", what, current, hipGetErrorString(back));
+    g_scratch_addr[dev].store(ptr, std::memory_order_release);
+  }
+  *addr = ptr;
+  return HEXKV_OK;
+}
+
+}  // namespace hexkv
+
+extern "C" int hexkv_attend(const hexkv_attend_params *p, void *workspace, size_t ws_bytes,
+                            hexkv_stream_t stream) {
+  hexkv::clear_error();
+  return hexkv::attend_launch(p, workspace, ws_bytes, stream, "hexkv_attend");
+}
+
+extern "C" int hexkv_attend_noalloc(const hexkv_attend_params *p, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_attend_noalloc";
+  int rc = validate(p);
+  if (rc != HEXKV_OK || p->batch == 0) return rc;
+  const size_t need = workspace_bytes(p, choose_partition(p));
+  if (need > HEXKV_NOALLOC_SCRATCH_BYTES)
+    return fail(HEXKV_EWORKSPACE,
+                "%s: this call needs %zu bytes of split-K workspace, above the %u-byte static scratch "
+                "(use hexkv_attend with a workspace, or fewer rows / a shorter max_seqlen)",
+                what, need, static_cast<unsigned>(HEXKV_NOALLOC_SCRATCH_BYTES));
+  void *ws = nullptr;
+  if (need > 0 && (rc = scratch_address(stream, &ws, what)) != HEXKV_OK) return rc;
+  return attend_launch(p, ws, need, stream, what);
 }
 
 // ------------------------------------------------------------ FT layout ---

@@ -288,6 +288,23 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     return out
 
 
+def decode_attention_noalloc(q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *, max_seqlen: int,
+                             seqlens: Optional[torch.Tensor] = None, seqlen_bias: int = 0,
+                             kv_new: Optional[torch.Tensor] = None, causal: bool = False,
+                             softmax_scale: Optional[float] = None, partition: int = 0,
+                             kernel: str = "auto") -> torch.Tensor:
+    """``decode_attention`` through ``hexkv_attend_noalloc``: no workspace and
+    no allocation (the split-K partials go to the library's static per-GPU
+    scratch of ``_lib.NOALLOC_SCRATCH_BYTES``); ``out`` is required.  Calls
+    on one GPU share that scratch, so overlapping calls on different streams
+    race.  Raises ValueError when the call needs more scratch than there is."""
+    _require_device(q, cache, out)
+    p = _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, causal,
+                       softmax_scale, partition, kernel)
+    _lib.check(_lib.load().hexkv_attend_noalloc(ctypes.byref(p), _stream(q)), "hexkv_attend_noalloc")
+    return out
+
+
 def ft_pack(dtype: torch.dtype) -> int:
     """Elements per 16-byte K chunk of the FT layout: 4 for float32, 8 for
     16-bit data (mha.py:423, generation.py:317)."""

@@ -201,6 +201,27 @@ int hexkv_attend_kernel(const hexkv_attend_params *p);
 int hexkv_attend(const hexkv_attend_params *p, void *workspace,
                  size_t workspace_bytes, hexkv_stream_t stream);
 
+/* Size of the static scratch array behind hexkv_attend_noalloc (per GPU). */
+#define HEXKV_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * hexkv_attend without a workspace argument: the same kernels and results,
+ * with the split-K partials in a static device array of
+ * HEXKV_NOALLOC_SCRATCH_BYTES (32 MiB) that the library holds on each GPU it
+ * runs on until the process ends.  The call allocates nothing (no hipMalloc,
+ * no library allocation); the caller still passes q, the cache and out.
+ * Returns HEXKV_EWORKSPACE when hexkv_attend_workspace_bytes(p) exceeds the
+ * array.  The array's address on a device is looked up on that device's
+ * first call (the stream's device; the current device for the null stream).
+ * Calls on one GPU share its array, which keeps the last call's contents:
+ * calls that overlap on one GPU (different streams, no ordering) race.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.
+ */
+int hexkv_attend_noalloc(const hexkv_attend_params *p, hexkv_stream_t stream);
+
 /*
  * The FasterTransformer ("FT") cache layout of hexgen_core's fused decode
  * path (fused_ft_kernel=True; the layout the reference's CUDA-graph decode

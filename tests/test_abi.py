@@ -163,3 +163,26 @@ def test_attend_kernel_rejects_bad_geometry():
     p.q_heads, p.kv_heads = 6, 4
     assert _lib.load().hexkv_attend_kernel(ctypes.byref(p)) == _lib.HEXKV_EINVAL
     assert b"q_heads" in _lib.load().hexkv_last_error()
+
+
+def test_noalloc_scratch_limit_matches_header_and_rejects_oversized_calls(tmp_path):
+    src = tmp_path / "limit.c"
+    src.write_text('#include <stdio.h>\n#include "hexkv.h"\n'
+                   'int main(void){ printf("%u\\n", HEXKV_NOALLOC_SCRATCH_BYTES); return 0; }\n')
+    exe = tmp_path / "limit"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)],
+                   check=True)
+    limit = int(subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout)
+    assert limit == _lib.NOALLOC_SCRATCH_BYTES
+    # A request whose split-K partials exceed the static scratch is refused on
+    # the host, before any HIP call: 4096 rows x 32 heads x 64 partitions.
+    lib = _lib.load()
+    p = _lib.AttendParams(dtype=_lib.HEXKV_BF16, batch=4096, q_len=1, q_heads=32, kv_heads=8, head_dim=128,
+                          softmax_scale=0.088, q=0x10000, q_batch_stride=32 * 128, q_row_stride=32 * 128,
+                          cache=0x20000, cache_batch_stride=8192 * 2048, cache_pos_stride=2048,
+                          cache_kv_stride=1024, capacity=8192, out=0x30000, out_batch_stride=32 * 128,
+                          out_row_stride=32 * 128, seqlen_bias=8192, max_seqlen=8192, partition=128)
+    need = lib.hexkv_attend_workspace_bytes(ctypes.byref(p))
+    assert need > limit
+    assert lib.hexkv_attend_noalloc(ctypes.byref(p), None) == _lib.HEXKV_EWORKSPACE
+    assert b"static scratch" in lib.hexkv_last_error()

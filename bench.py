@@ -47,7 +47,7 @@ def log(msg):
 class Job:
     """Device buffers of one workload and the timed job pass."""
 
-    def __init__(self, w, device, kernel="auto"):
+    def __init__(self, w, device, kernel="auto", grid=False):
         self.w = w
         self.kernel = kernel
         L, B, S = w.layers, w.batch, w.capacity
@@ -64,9 +64,12 @@ class Job:
         self.out = torch.empty((B, 1, w.q_heads, w.head_dim), dtype=w.dtype, device=device)
         self.seqlens = torch.tensor(w.lens, dtype=torch.int32, device=device)
         self.max_len = max(w.lens)
+        # Decode steps run the host-planned work list (the lengths are known
+        # here): one list per step, shared by every layer.
         self.plan = ops.AttendPlan(self.q[0], self.decode_layers[0], self.out,
                                    max_seqlens=[self.max_len + t + 1 for t in range(w.decode_steps)],
-                                   seqlens=self.seqlens, kv_new=self.kv_new[0], kernel=kernel)
+                                   seqlens=self.seqlens, kv_new=self.kv_new[0], kernel=kernel,
+                                   lens=None if grid else w.lens)
         self.kernel_name = ops.attend_kernel(self.q[0], self.decode_layers[0], kernel)
         self.positions = self.seqlens.clone()
         self.graph = None
@@ -415,6 +418,8 @@ def main():
     ap.add_argument("--no-formats", action="store_true", help="skip the legacy-format figures")
     ap.add_argument("--kernel", default="auto", choices=("auto", "valu", "mfma"),
                     help="attention kernel (auto: the library's choice for the workload)")
+    ap.add_argument("--grid", action="store_true",
+                    help="decode attention over the library's uniform partitions instead of the work list")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the short dispatch sequence for hardware-counter runs")
     args = ap.parse_args()
@@ -425,7 +430,7 @@ def main():
     device = torch.device("cuda", 0)
     w = workload(args.workload)
     log(f"workload {w.describe()}")
-    job = Job(w, device, args.kernel)
+    job = Job(w, device, args.kernel, grid=args.grid)
     log(f"buffers ready; attention kernel {job.kernel_name}")
     if args.traffic_probe:
         job.traffic_probe()
@@ -488,6 +493,7 @@ def main():
         "dtype": str(w.dtype).split(".")[-1].replace("bfloat16", "bf16").replace("float16", "fp16"),
         "data": "synthetic (seeded N(0,1) K/V, seeded ragged lengths)",
         "config": {**w.describe(), "attention_kernel": job.kernel_name,
+                   "attention_schedule": "uniform grid" if args.grid else "work list (hexkv_attend_plan)",
                    "parallelism": "single GPU (prefill and decode share it)"},
         "pack_unpack_ms": round(pu_ms, 3),
         "pack_unpack_hbm_frac": round(pu_gbs / HBM_PEAK_GBS, 4),

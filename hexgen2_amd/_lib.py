@@ -22,7 +22,7 @@ EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "h
            "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
            "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend",
-           "hexkv_attend_noalloc")
+           "hexkv_attend_noalloc", "hexkv_attend_plan")
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
@@ -39,7 +39,16 @@ class AttendParams(ctypes.Structure):
         ("out", ctypes.c_void_p), ("out_batch_stride", ctypes.c_int64), ("out_row_stride", ctypes.c_int64),
         ("seqlens_dev", ctypes.c_void_p), ("seqlen_bias", ctypes.c_int32), ("max_seqlen", ctypes.c_int32),
         ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int), ("kernel", ctypes.c_int),
+        ("work_items_dev", ctypes.c_void_p), ("work_parts_dev", ctypes.c_void_p),
+        ("n_work_items", ctypes.c_int32), ("work_max_parts", ctypes.c_int32),
     ]
+
+
+class WorkItem(ctypes.Structure):
+    """Mirror of ``hexkv_work_item`` (32 bytes)."""
+    _fields_ = [("row", ctypes.c_int32), ("head_group", ctypes.c_int32), ("part", ctypes.c_int32),
+                ("parts", ctypes.c_int32), ("first", ctypes.c_int32), ("count", ctypes.c_int32),
+                ("len", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class FtAttendParams(ctypes.Structure):
@@ -102,6 +111,10 @@ def load() -> ctypes.CDLL:
     lib.hexkv_attend_kernel.argtypes = [ctypes.POINTER(AttendParams)]
     lib.hexkv_attend.restype = ci
     lib.hexkv_attend.argtypes = [ctypes.POINTER(AttendParams), vp, ctypes.c_size_t, vp]
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    lib.hexkv_attend_plan.restype = ci
+    lib.hexkv_attend_plan.argtypes = [ctypes.POINTER(AttendParams), vp, vp, ctypes.c_int32, vp, ctypes.c_int32,
+                                      i32p, i32p]
     lib.hexkv_attend_noalloc.restype = ci
     lib.hexkv_attend_noalloc.argtypes = [ctypes.POINTER(AttendParams), vp]
     blocks = ctypes.POINTER(Block)

@@ -49,6 +49,8 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 namespace hexkv {
 
@@ -79,6 +81,16 @@ struct AttendArgs {
   float scale_log2;    // softmax_scale * log2(e), > 0
   float *ws_o;         // [rows][q_heads][max_parts][D]
   float *ws_ml;        // [rows][q_heads][max_parts][2]
+  // Work-list mode (items != nullptr, decode rows only): workgroup i runs
+  // items[i], which carries its row's length, so the kernel reads no
+  // seqlens; seg_parts[row * n_groups + head group] is that segment's
+  // partition count for the merge (partitions of one segment may differ in
+  // size).  Grid mode otherwise: grid (partition, head group, row),
+  // partitions of `part` positions, lengths from seqlens.
+  const hexkv_work_item *items;
+  const int32_t *seg_parts;
+  int32_t n_groups;
+  int32_t rows;  // query rows (batch * q_len)
   // FasterTransformer cache layouts (hexkv_ft_attend only): K is
   // [batch][kv_heads][D / pack][capacity][pack] (one 16-byte chunk of D per
   // position), V is [batch][kv_heads][capacity][D]; strides in bytes.  The
@@ -125,13 +137,36 @@ struct Work {
 // writing the defined zero output of an empty row).
 template <typename T, int D, int G>
 __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
-  w.row = blockIdx.z;
-  w.b = w.row / a.q_len;
-  w.t = w.row - w.b * a.q_len;
-  w.len = row_length(a, w.b, w.t, &w.pos_new);
-  w.part = blockIdx.x;
-  w.p0 = w.part * a.part;
-  w.qh0 = blockIdx.y * G;
+  int hg;
+  if (a.items) {
+    const hexkv_work_item it = a.items[blockIdx.x];
+    // Items come from device memory: one naming a row, head group, partition
+    // or positions outside this call's geometry does nothing.
+    if (static_cast<unsigned>(it.row) >= static_cast<unsigned>(a.rows) ||
+        static_cast<unsigned>(it.head_group) >= static_cast<unsigned>(a.n_groups) ||
+        static_cast<unsigned>(it.part) >= static_cast<unsigned>(a.max_parts) || it.parts < 1 ||
+        it.parts > a.max_parts || it.first < 0 || it.count < 0 || it.len > a.max_seqlen ||
+        it.first + it.count > it.len)
+      return false;
+    w.row = w.b = it.row;
+    w.t = 0;
+    hg = it.head_group;
+    w.part = it.part;
+    w.nparts = it.parts;
+    w.p0 = it.first;
+    w.n = it.count;
+    w.len = it.len;
+    w.pos_new = a.kv_new ? w.len - 1 : -1;
+  } else {
+    w.row = blockIdx.z;
+    w.b = w.row / a.q_len;
+    w.t = w.row - w.b * a.q_len;
+    w.len = row_length(a, w.b, w.t, &w.pos_new);
+    hg = blockIdx.y;
+    w.part = blockIdx.x;
+    w.p0 = w.part * a.part;
+  }
+  w.qh0 = hg * G;
   if (w.len <= 0) {
     if (w.part == 0) {
       T *out_row = static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D;
@@ -139,9 +174,13 @@ __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
     }
     return false;
   }
-  if (w.p0 >= w.len) return false;
-  w.n = min(a.part, w.len - w.p0);
-  w.nparts = (w.len + a.part - 1) / a.part;
+  if (!a.items) {
+    if (w.p0 >= w.len) return false;
+    w.n = min(a.part, w.len - w.p0);
+    w.nparts = (w.len + a.part - 1) / a.part;
+  } else if (w.n <= 0) {
+    return false;
+  }
   w.hk = w.qh0 / a.group;
   // The new row, when attended at all, is the row's last position.
   w.has_new = a.kv_new != nullptr && w.pos_new == w.p0 + w.n - 1;
@@ -910,9 +949,14 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
 
   if constexpr (PER == 1) {
     if (a.max_parts <= kCombineChunk && a.max_parts <= SL * kCombineDepth) {
-      int pos_new;
-      const int len = row_length(a, b, t, &pos_new);
-      const int nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
+      int nparts;
+      if (a.items) {
+        nparts = min(a.seg_parts[row * a.n_groups + h / G], a.max_parts);
+      } else {
+        int pos_new;
+        const int len = row_length(a, b, t, &pos_new);
+        nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
+      }
       if (nparts <= 1) return;  // written by the attention kernel
       const bool valid = tid < nparts;
       float2 mlv = {-INFINITY, 0.f};
@@ -962,10 +1006,14 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
     }
   }
 
-  int pos_new;
-  const int len = row_length(a, b, t, &pos_new);
-  if (len <= 0) return;
-  const int nparts = (len + a.part - 1) / a.part;
+  int nparts;
+  if (a.items) {
+    nparts = min(a.seg_parts[row * a.n_groups + h / G], a.max_parts);
+  } else {
+    int pos_new;
+    const int len = row_length(a, b, t, &pos_new);
+    nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
+  }
   if (nparts <= 1) return;
   if (tid < 64) {
     float mx = kNoScore;
@@ -1056,7 +1104,10 @@ static int choose_partition(const hexkv_attend_params *p) {
   return part;
 }
 
+// Partitions per (row, head group) the workspace holds: from the work list
+// when there is one, else from the partition size and max_seqlen.
 static int64_t max_parts_of(const hexkv_attend_params *p, int part) {
+  if (p->work_items_dev) return std::max<int64_t>(1, p->work_max_parts);
   return std::max<int64_t>(1, (p->max_seqlen + part - 1) / part);
 }
 
@@ -1095,6 +1146,15 @@ static int validate(const hexkv_attend_params *p) {
     return fail(HEXKV_EINVAL, "hexkv_attend: unknown kernel %d", p->kernel);
   if (p->kernel == HEXKV_KERNEL_MFMA && (p->dtype == HEXKV_F32 || p->head_dim < 64))
     return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the MFMA kernel takes float16/bfloat16 with head_dim >= 64");
+  if (p->work_items_dev) {
+    if (p->n_work_items < 1 || !p->work_parts_dev || p->work_max_parts < 1 || p->work_max_parts > 65535)
+      return fail(HEXKV_EINVAL, "hexkv_attend: a work list needs n_work_items >= 1, work_parts_dev and "
+                                "1 <= work_max_parts <= 65535");
+    if (!aligned16(p->work_items_dev) || (reinterpret_cast<uintptr_t>(p->work_parts_dev) & 3u))
+      return fail(HEXKV_EINVAL, "hexkv_attend: work_items_dev must be 16-byte aligned, work_parts_dev 4-byte");
+    if (p->q_len != 1 || p->causal)
+      return fail(HEXKV_EINVAL, "hexkv_attend: a work list is for decode rows (q_len 1, not causal)");
+  }
   if (p->batch == 0) return HEXKV_OK;
   if (!p->q || !p->cache || !p->out) return fail(HEXKV_EINVAL, "hexkv_attend: null tensor");
   const int vec = 16 / elem_size(p->dtype);
@@ -1148,7 +1208,7 @@ static void launch(const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
     attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
   }
   if (a.max_parts > 1) {
-    const dim3 cgrid(a.q_heads, grid.z);
+    const dim3 cgrid(a.q_heads, a.rows);
     constexpr int SL = kAttThreads / D >= 1 ? kAttThreads / D : 1;
     if (a.max_parts <= 8 * SL) combine_kernel<T, D, G, 8><<<cgrid, kAttThreads, 0, s>>>(a);
     else combine_kernel<T, D, G, 32><<<cgrid, kAttThreads, 0, s>>>(a);
@@ -1180,6 +1240,116 @@ static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, int kind, hi
 }
 
 }  // namespace hexkv
+
+namespace hexkv {
+
+// Chunk size (positions) of a work list when the caller leaves the choice to
+// the library, by the bytes one call reads (W positions over all (row, head
+// group) segments, row_bytes per position of one KV head).  Measured on
+// MI355X against the uniform grid and against each other (attention +
+// merge per layer, interleaved A/B in one process): below 4 MB the call is
+// launch-bound and no split at all is fastest (TinyLlama: 6.5 vs 8.1 us --
+// no merge launch); up to 64 MB it is latency-bound and about 200 items,
+// one per CU, are fastest (the Llama-2-70B TP-8 share: 384-position chunks
+// 13.3 us against 15.2 for the grid, 14.9 at 256, 14.7 at 512); above,
+// 1024-position chunks (Llama-3-8B 170-173 us against 179 for the grid and
+// 179.6 at 512; Llama-2-7B 31.4 against 33.6 for the grid and 34.6 at 1280).
+static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest) {
+  const int64_t bytes = positions * row_bytes;
+  if (bytes < (INT64_C(4) << 20)) return static_cast<int>(std::max<int64_t>(64, (longest + 63) / 64 * 64));
+  if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 200 + 63) / 64 * 64)));
+  return 1024;
+}
+
+}  // namespace hexkv
+
+extern "C" int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_work_item *items,
+                                 int32_t items_capacity, int32_t *parts, int32_t parts_capacity,
+                                 int32_t *n_items, int32_t *max_parts) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_attend_plan";
+  if (!p || !lens || !n_items || !max_parts) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  if (p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads || p->batch < 0 || p->batch > 65535)
+    return fail(HEXKV_EINVAL, "%s: bad batch or head counts", what);
+  if (p->q_len != 1 || p->causal) return fail(HEXKV_EINVAL, "%s: work lists are for decode rows (q_len 1, not causal)", what);
+  if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > 4096)))
+    return fail(HEXKV_EINVAL, "%s: partition must be 0 or a multiple of 64 up to 4096", what);
+  const int G = kernel_group(p->q_heads / p->kv_heads);
+  const int groups = p->q_heads / G;
+  const int64_t segs = static_cast<int64_t>(p->batch) * groups;
+  const int extra = p->kv_new ? 1 : 0;
+  int64_t positions = 0, longest = 0;
+  for (int b = 0; b < p->batch; ++b) {
+    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+    if (len < 0 || len > p->max_seqlen)
+      return fail(HEXKV_ERANGE, "%s: row %d attends %lld keys, outside [0, max_seqlen %d]", what, b,
+                  static_cast<long long>(len), p->max_seqlen);
+    positions += len * groups;
+    longest = std::max(longest, len);
+  }
+  const int64_t row_bytes = 2 * static_cast<int64_t>(p->head_dim) * elem_size(p->dtype);
+  const int64_t chunk = p->partition > 0 ? p->partition : plan_chunk(positions, row_bytes, longest);
+  int64_t count = 0, most = 1, full_rounds = 0;
+  for (int b = 0; b < p->batch; ++b) {
+    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+    const int64_t k = len == 0 ? 1 : (len + chunk - 1) / chunk;
+    count += k * groups;
+    most = std::max(most, k);
+    full_rounds = std::max(full_rounds, len / chunk);
+  }
+  if (most > 65535 || count > INT32_MAX) return fail(HEXKV_EUNSUPPORTED, "%s: more than 65535 partitions per row", what);
+  *n_items = static_cast<int32_t>(count);
+  *max_parts = static_cast<int32_t>(most);
+  if (!items) return HEXKV_OK;  // a size query
+  if (items_capacity < count || !parts || parts_capacity < segs)
+    return fail(HEXKV_EINVAL, "%s: room for %d items and %d segment counts given, %lld and %lld needed", what,
+                items_capacity, parts_capacity, static_cast<long long>(count), static_cast<long long>(segs));
+  // Order: empty rows (a zero output each), then the full chunks, chunk index
+  // by chunk index across all (row, head group) segments, then every row's
+  // last, shorter chunk from the longest down, so the launch ends on its
+  // smallest items.
+  int64_t n = 0;
+  auto put = [&](int b, int hg, int64_t part, int64_t k, int64_t first, int64_t cnt, int64_t len) {
+    hexkv_work_item &it = items[n++];
+    it.row = b;
+    it.head_group = hg;
+    it.part = static_cast<int32_t>(part);
+    it.parts = static_cast<int32_t>(k);
+    it.first = static_cast<int32_t>(first);
+    it.count = static_cast<int32_t>(cnt);
+    it.len = static_cast<int32_t>(len);
+    it.reserved = 0;
+  };
+  std::vector<std::pair<int64_t, int64_t>> tails;  // (positions, b * groups + hg)
+  for (int b = 0; b < p->batch; ++b) {
+    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+    const int64_t k = len == 0 ? 1 : (len + chunk - 1) / chunk;
+    for (int hg = 0; hg < groups; ++hg) {
+      parts[static_cast<int64_t>(b) * groups + hg] = static_cast<int32_t>(k);
+      if (len == 0) put(b, hg, 0, 1, 0, 0, 0);
+      else if (len % chunk) tails.emplace_back(len % chunk, static_cast<int64_t>(b) * groups + hg);
+    }
+  }
+  for (int64_t c = 0; c < full_rounds; ++c)
+    for (int b = 0; b < p->batch; ++b) {
+      const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+      if ((c + 1) * chunk > len) continue;
+      const int64_t k = (len + chunk - 1) / chunk;
+      for (int hg = 0; hg < groups; ++hg) put(b, hg, c, k, c * chunk, chunk, len);
+    }
+  std::stable_sort(tails.begin(), tails.end(),
+                   [](const std::pair<int64_t, int64_t> &x, const std::pair<int64_t, int64_t> &y) { return x.first > y.first; });
+  for (const auto &t : tails) {
+    const int b = static_cast<int>(t.second / groups), hg = static_cast<int>(t.second % groups);
+    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+    const int64_t k = (len + chunk - 1) / chunk;
+    put(b, hg, k - 1, k, (k - 1) * chunk, t.first, len);
+  }
+  if (n != count) return fail(HEXKV_EINVAL, "%s: internal count mismatch %lld vs %lld", what,
+                              static_cast<long long>(n), static_cast<long long>(count));
+  return HEXKV_OK;
+}
 
 extern "C" size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p) {
   using namespace hexkv;
@@ -1247,14 +1417,23 @@ static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t w
     a.ws_o = static_cast<float *>(workspace);
     a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
   }
+  a.n_groups = p->q_heads / G;
+  a.rows = static_cast<int32_t>(rows);
+  a.items = p->work_items_dev;
+  a.seg_parts = p->work_parts_dev;
 
-  // Workgroups reach the 8 XCDs round-robin by linear index, and the later
-  // partitions exist only in long rows.  With an even partition count the
-  // same partition indices would always land on the same XCDs (measured 1.6x
-  // slower at 32 than at 31); an odd count rotates them across the XCDs from
-  // one (head group, row) to the next.  The extra column is empty.
-  const unsigned grid_x = static_cast<unsigned>(max_parts | 1);
-  dim3 grid(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));
+  dim3 grid;
+  if (a.items) {
+    grid = dim3(static_cast<unsigned>(p->n_work_items));  // one workgroup per item, in list order
+  } else {
+    // Workgroups reach the 8 XCDs round-robin by linear index, and the later
+    // partitions exist only in long rows.  With an even partition count the
+    // same partition indices would always land on the same XCDs (measured
+    // 1.6x slower at 32 than at 31); an odd count rotates them across the
+    // XCDs from one (head group, row) to the next.  The extra column is empty.
+    const unsigned grid_x = static_cast<unsigned>(max_parts | 1);
+    grid = dim3(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int kind = use_mfma(p, G) ? kLaunchMfma : kLaunchValu;
   switch (p->dtype) {
@@ -1448,6 +1627,8 @@ extern "C" int hexkv_ft_attend(const hexkv_ft_attend_params *p, void *workspace,
     a.ws_o = static_cast<float *>(workspace);
     a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
   }
+  a.rows = static_cast<int32_t>(rows);
+  a.n_groups = p->q_heads / G;
   a.k_ft = p->k_cache;
   a.v_ft = p->v_cache;
   a.k_ft_head = d * cap * es;  // D / pack chunks of capacity x 16 bytes

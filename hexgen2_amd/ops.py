@@ -257,7 +257,7 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
                      kv_new: Optional[torch.Tensor] = None, causal: bool = False,
                      softmax_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
                      workspace: Optional[torch.Tensor] = None, partition: int = 0,
-                     kernel: str = "auto") -> torch.Tensor:
+                     kernel: str = "auto", lens: Optional[Sequence[int]] = None) -> torch.Tensor:
     """Attention of ``q [B, q_len, Hq, D]`` over a cache ``[B, S, 2, Hkv, D]``.
 
     Sequence b attends to ``len_b = seqlens[b] + seqlen_bias`` keys (the
@@ -268,7 +268,9 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     ``h // (Hq // Hkv)`` (mha.py:223-224); ``softmax_scale`` defaults to
     ``D ** -0.5`` (gpt.py:72).  ``kernel`` picks the score kernel: "valu"
     (packed dot products), "mfma" (the GQA group on the matrix cores, 16-bit
-    only) or "auto" (the library's choice).
+    only) or "auto" (the library's choice).  ``lens``, the host values of
+    ``seqlens`` (decode rows), makes the call run a work list
+    (``hexkv_attend_plan``; ``partition`` then sets its chunk size).
     """
     _require_device(q, cache)
     if out is None:
@@ -276,6 +278,10 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     p = _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, causal,
                        softmax_scale, partition, kernel)
     lib = _lib.load()
+    work = None
+    if lens is not None:
+        work = _plan_work(p, lens, q.device)  # kept alive until the launch is enqueued
+        work.apply(p)
     need = int(lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
     ws_ptr, ws_bytes = None, 0
     if need:
@@ -286,6 +292,40 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     rc = lib.hexkv_attend(ctypes.byref(p), ws_ptr, ws_bytes, _stream(q))
     _lib.check(rc, "hexkv_attend")
     return out
+
+
+class WorkList:
+    """A ``hexkv_attend_plan`` work list in device memory: ``items``
+    (``[n_items, 8]`` int32, one ``hexkv_work_item`` per workgroup) and
+    ``parts`` (partitions per (row, head group)), valid for the lengths and
+    ``seqlen_bias``/``max_seqlen`` it was built for."""
+
+    def __init__(self, items: torch.Tensor, parts: torch.Tensor, n_items: int, max_parts: int):
+        self.items, self.parts, self.n_items, self.max_parts = items, parts, n_items, max_parts
+
+    def apply(self, p: _lib.AttendParams) -> None:
+        p.work_items_dev, p.work_parts_dev = self.items.data_ptr(), self.parts.data_ptr()
+        p.n_work_items, p.work_max_parts = self.n_items, self.max_parts
+
+
+def _plan_work(p: _lib.AttendParams, lens: Sequence[int], device) -> WorkList:
+    """Build the work list on the host (``hexkv_attend_plan``) and copy it to
+    ``device`` on the current stream (asynchronously, from pinned memory)."""
+    lib = _lib.load()
+    if len(lens) != p.batch:
+        raise ValueError(f"{len(lens)} host lengths for a batch of {p.batch}")
+    c_lens = (ctypes.c_int32 * len(lens))(*[int(n) for n in lens])
+    n_items, max_parts = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n_items),
+                                     ctypes.byref(max_parts)), "hexkv_attend_plan")
+    n_segs = p.batch * p.q_heads  # head groups never outnumber query heads
+    items = torch.empty((max(n_items.value, 1), 8), dtype=torch.int32, pin_memory=True)
+    parts = torch.empty(max(n_segs, 1), dtype=torch.int32, pin_memory=True)
+    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, ctypes.c_void_p(items.data_ptr()), items.shape[0],
+                                     ctypes.c_void_p(parts.data_ptr()), parts.shape[0], ctypes.byref(n_items),
+                                     ctypes.byref(max_parts)), "hexkv_attend_plan")
+    return WorkList(items.to(device, non_blocking=True), parts.to(device, non_blocking=True),
+                    n_items.value, max_parts.value)
 
 
 def decode_attention_noalloc(q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *, max_seqlen: int,
@@ -474,20 +514,43 @@ class AttendPlan:
     def __init__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *,
                  max_seqlens: Sequence[int], seqlens: Optional[torch.Tensor] = None,
                  kv_new: Optional[torch.Tensor] = None, softmax_scale: Optional[float] = None,
-                 partition: int = 0, kernel: str = "auto"):
+                 partition: int = 0, kernel: str = "auto", lens: Optional[Sequence[int]] = None):
+        """``lens``: the host values of ``seqlens`` (decode rows).  With them
+        each call runs a work list (``hexkv_attend_plan``: compact, largest
+        items first) built once per (``seqlen_bias``, ``max_seqlen``) and
+        shared by every layer called with the same pair; without them the
+        library's uniform partitions over the device lengths."""
         _require_device(q, cache, out)
         self.params = _attend_params(q, cache, out, seqlens, 0, max(max_seqlens), kv_new, False,
                                      softmax_scale, partition, kernel)
         self.lib = _lib.load()
         need = 0
-        for m in max_seqlens:
-            self.params.max_seqlen = int(m)
-            need = max(need, int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params))))
+        if lens is None:
+            for m in max_seqlens:
+                self.params.max_seqlen = int(m)
+                need = max(need, int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params))))
         self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
         self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), self.workspace.numel()
         self.device = q.device
         self.fused = kv_new is not None
         self.geometry = _plan_geometry(q, cache, out, kv_new)
+        self.lens = None if lens is None else [int(n) for n in lens]
+        self.work_key, self.work = None, None
+
+    def _use_work_list(self, seqlen_bias: int, max_seqlen: int) -> None:
+        """Point the parameter block at the work list for this step (built
+        on first use) and grow the workspace if the list needs more."""
+        p = self.params
+        key = (int(seqlen_bias), int(max_seqlen))
+        if key != self.work_key:
+            p.work_items_dev = None
+            self.work = _plan_work(p, self.lens, self.device)
+            self.work_key = key
+        self.work.apply(p)
+        need = int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
+        if need > self.ws_bytes:
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+            self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), need
 
     def check(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
               kv_new: Optional[torch.Tensor]) -> None:
@@ -502,6 +565,8 @@ class AttendPlan:
         if kv_new is not None:
             p.kv_new = kv_new.data_ptr()
         p.seqlen_bias, p.max_seqlen = int(seqlen_bias), int(max_seqlen)
+        if self.lens is not None:
+            self._use_work_list(seqlen_bias, max_seqlen)
         _lib.check(self.lib.hexkv_attend(ctypes.byref(p), self.ws_ptr, self.ws_bytes, _stream(q)),
                    "hexkv_attend")
         return out

@@ -136,6 +136,19 @@ int hexkv_append(const void *kv_new, void *cache, int batch,
                  hexkv_stream_t stream);
 
 /*
+ * One workgroup's share of decode attention in a work list (32 bytes): the
+ * `count` positions from `first` of query row `row` for the query heads of
+ * head group `head_group` (head groups of hexkv_attend_plan's size), which
+ * is partition `part` of the `parts` partitions that row and head group is
+ * cut into.  `len` is the row's attended length (with kv_new, the new row
+ * is position len - 1).
+ */
+typedef struct hexkv_work_item {
+  int32_t row, head_group, part, parts;
+  int32_t first, count, len, reserved;
+} hexkv_work_item;
+
+/*
  * Geometry and inputs of one attention call.  Strides are in elements.
  * Query row r = (b, t), b < batch, t < q_len; q and out are
  * [batch][q_len][q_heads][head_dim] with the two innermost dims contiguous.
@@ -173,6 +186,17 @@ typedef struct hexkv_attend_params {
   int partition;
   /* enum hexkv_kernel: which kernel computes the scores. */
   int kernel;
+  /* Optional work list (device memory, from hexkv_attend_plan), decode rows
+   * only (q_len 1, not causal): one workgroup per item, in list order.  The
+   * items carry the row lengths, so seqlens_dev and seqlen_bias are not
+   * read.  work_parts_dev[row * head_groups + head group] is the partition
+   * count of that (row, head group) for the split merge; work_max_parts
+   * bounds every count and sizes the workspace.  NULL: the library's
+   * uniform partitions over the lengths in seqlens_dev. */
+  const hexkv_work_item *work_items_dev;
+  const int32_t *work_parts_dev;
+  int32_t n_work_items;
+  int32_t work_max_parts;
 } hexkv_attend_params;
 
 /* Workspace bytes hexkv_attend needs for these parameters (0 when one
@@ -200,6 +224,32 @@ int hexkv_attend_kernel(const hexkv_attend_params *p);
  */
 int hexkv_attend(const hexkv_attend_params *p, void *workspace,
                  size_t workspace_bytes, hexkv_stream_t stream);
+
+/*
+ * Work list for hexkv_attend over decode rows whose lengths the host knows:
+ * row b attends len_b = lens[b] + p->seqlen_bias (+1 with kv_new) keys,
+ * each within [0, p->max_seqlen].  Every (row, head group) segment is cut
+ * into chunks of p->partition positions (0: the library's choice by the
+ * bytes the call reads), and the items are ordered for the launch: empty
+ * rows, then the full chunks across all segments, then each segment's last,
+ * shorter chunk from the longest down.  Host memory only; the caller copies
+ * `items` and `parts` to the device and passes them in
+ * hexkv_attend_params.work_*.
+ *
+ *   lens            host int32 [batch]
+ *   items, parts    host outputs: up to items_capacity items and
+ *                   parts_capacity (>= batch * head groups) partition counts;
+ *                   items == NULL only sizes the plan
+ *   n_items, max_parts   outputs: the item count and the largest partition
+ *                   count (work_max_parts)
+ *
+ * The reference has no planning step: this replaces nothing in it.  It is
+ * how the call of mha.py:568-569 (FlashCrossAttention over the cache) is
+ * cut into workgroups when the lengths are known on the host.
+ */
+int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_work_item *items,
+                      int32_t items_capacity, int32_t *parts, int32_t parts_capacity,
+                      int32_t *n_items, int32_t *max_parts);
 
 /* Size of the static scratch array behind hexkv_attend_noalloc (per GPU). */
 #define HEXKV_NOALLOC_SCRATCH_BYTES (32u << 20)

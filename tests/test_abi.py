@@ -30,13 +30,17 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
     assert lib.hexkv_version() >= 100
+    # a successful call clears the thread's last error
+    p = _lib.AttendParams(q_heads=8, kv_heads=2, kernel=0)
+    assert lib.hexkv_attend_kernel(ctypes.byref(p)) == 1
     assert lib.hexkv_last_error() == b""
 
 
 @pytest.mark.parametrize("c_name,mirror", [("hexkv_attend_params", _lib.AttendParams),
                                             ("hexkv_ft_attend_params", _lib.FtAttendParams),
                                             ("hexkv_block", _lib.Block),
-                                            ("hexkv_ipc_handle", _lib.IpcHandle)])
+                                            ("hexkv_ipc_handle", _lib.IpcHandle),
+                                            ("hexkv_work_item", _lib.WorkItem)])
 def test_struct_layouts_match_c(tmp_path, c_name, mirror):
     fields = [f[0] for f in mirror._fields_]
     src = tmp_path / "layout.c"

@@ -131,8 +131,15 @@ def test_batch_pad_cases(emu, run):
 
 def test_head_concat_gather_and_fallback(emu, run):
     v0 = emu.emu_violations()
-    # one-head TP-8 shards, separate tensors per layer: one gather launch per layer
-    shards = [{l: rand((4, 300, 2, 1, 128), torch.bfloat16, 10 * j + l) for l in range(3)} for j in range(8)]
+    # one-head TP-8 shards, separate tensors per layer: one gather launch per
+    # layer.  Each layer's shard is a view into its own buffer at an uneven
+    # offset, so no two layers sit a fixed stride apart (which would let the
+    # host fold them into one launch).
+    base = [rand((4 * 300 * 2 * 128 + 64 * (l + 1) * (l + 2),), torch.bfloat16, 90 + l) for l in range(3)]
+    shards = [{l: base[l][64 * (l + 1) * (l + 2) // 2:][:4 * 300 * 2 * 128].view(4, 300, 2, 1, 128)
+               if j == 0 else rand((4, 300, 2, 1, 128), torch.bfloat16, 10 * j + l) for l in range(3)}
+              for j in range(8)]
+    run(*base)
     run(*[t for d in shards for t in d.values()])
     launches = emu.emu_launches()
     got = kvf.concat_dicts(shards)

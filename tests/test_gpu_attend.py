@@ -236,3 +236,62 @@ def test_validation_errors(device):
         ops.decode_attention(qq, cc, max_seqlen=4, seqlen_bias=4, kernel="mfma")  # fp32
     with pytest.raises(ValueError):
         ops.decode_attention(q, cache, max_seqlen=4, seqlen_bias=4, softmax_scale=-1.0)
+
+
+# ------------------------------------------------------------- work lists ---
+# hexkv_attend_plan's list (compact, largest items first, lengths carried by
+# the items) against the oracle: every geometry, both kernels, the library's
+# chunk choice and forced chunks, with and without the fused append.
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel", CASES)
+def test_work_list_ragged_within_tolerance(device, hq, hkv, d, dtype, kernel):
+    lens = [0, 1, 15, 16, 17, 63, 64, 65, 700, 1500, 2047, 2048]
+    cap = 2112
+    print(f"work list {kernel} hq={hq} hkv={hkv} d={d} {dtype}", flush=True)
+    q, cache = make(len(lens), cap, hq, hkv, d, dtype, 41, device)
+    g = torch.Generator(device=device).manual_seed(42)
+    kv_new = torch.randn((len(lens), 2, hkv, d), generator=g, device=device).to(dtype)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    before = bits(cache)
+    want_cache = oracle.append(before, bits(kv_new), lens)
+    for partition in (0, 64, 384, 1024):
+        c = cache.clone()
+        out = ops.decode_attention(q, c, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new,
+                                   partition=partition, kernel=kernel, lens=lens)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(c), want_cache)
+        check(out, q, c, [n + 1 for n in lens], dtype)
+    # without the append: the empty row gives zeros
+    out = torch.full_like(q, 9.0)
+    ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, kernel=kernel, lens=lens, out=out)
+    assert (out[0] == 0).all()
+    check(out[1:], q[1:], cache[1:], lens[1:], dtype)
+
+
+@pytest.mark.parametrize("kernel", ["valu", "mfma"])
+def test_attend_plan_work_list_matches_grid_over_steps(device, kernel):
+    # AttendPlan with host lengths (a list per step, shared by the layers)
+    # against the same plan over the device lengths only (uniform grid)
+    lens = [300, 5, 1200, 77, 2500, 640]
+    L, steps = 3, 4
+    cap = max(lens) + steps
+    g = torch.Generator(device=device).manual_seed(43)
+    q = torch.randn((L, len(lens), 1, 32, 128), generator=g, device=device).to(torch.bfloat16)
+    kv = torch.randn((L, len(lens), 2, 8, 128), generator=g, device=device).to(torch.bfloat16)
+    caches = torch.randn((L, len(lens), cap, 2, 8, 128), generator=g, device=device).to(torch.bfloat16)
+    c_list, c_grid = caches.clone(), caches.clone()
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    o_list, o_grid = torch.empty_like(q[0]), torch.empty_like(q[0])
+    maxes = [max(lens) + t + 1 for t in range(steps)]
+    p_list = ops.AttendPlan(q[0], c_list[0], o_list, max_seqlens=maxes, seqlens=seqlens, kv_new=kv[0],
+                            kernel=kernel, lens=lens)
+    p_grid = ops.AttendPlan(q[0], c_grid[0], o_grid, max_seqlens=maxes, seqlens=seqlens, kv_new=kv[0],
+                            kernel=kernel)
+    for t in range(steps):
+        for l in range(L):
+            p_list(q[l], c_list[l], o_list, kv[l], t, maxes[t])
+            p_grid(q[l], c_grid[l], o_grid, kv[l], t, maxes[t])
+            torch.cuda.synchronize()
+            torch.testing.assert_close(o_list.float(), o_grid.float(), rtol=0, atol=8e-3)
+            check(o_list, q[l], c_list[l], [n + t + 1 for n in lens], torch.bfloat16)
+    assert torch.equal(c_list.view(torch.int16), c_grid.view(torch.int16))

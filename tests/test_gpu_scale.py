@@ -8,11 +8,11 @@ bf16, one KV head per 8 query heads) and Llama-3-8B (64 rows of U[128, 8192],
 bf16), each at the first and at the last decode step, where the longest
 rows reach the cache capacity (8153 positions in the seeded Llama-3-8B draw:
 16 partitions of 512).  Both score kernels run every case with the library's
-partition choice, and again with 128-position partitions (up to 64 per row:
-the combine kernel's deep register path).  The append is checked bit-exactly
-against the oracle over
-the whole layer (the new row at each sequence's position, every other byte
-unchanged); attention within 2e-3 (fp16) / 8e-3 (bf16) max-abs.
+partition choice, again with 128-position partitions (up to 64 per row:
+the combine kernel's deep register path), and with the host-planned work
+list (hexkv_attend_plan).  The append is checked bit-exactly against the
+oracle over the whole layer (the new row at each sequence's position, every
+other byte unchanged); attention within 2e-3 (fp16) / 8e-3 (bf16) max-abs.
 
 The full Llama-3-8B handoff -- pack of all 32 layers' live rows (243,613
 rows of 4 KB per layer, 31.9 GB) and unpack into a sentinel-filled decode
@@ -67,13 +67,14 @@ def test_decode_step_at_full_size(device, name, step):
     want_cache = oracle.append(bits(base), bits(kv_new), pos)
     outs = {}
     for kernel in ("valu", "mfma"):
-        for partition in (0, 128):
+        for partition, lens in ((0, None), (128, None), (0, pos)):
+            mode = f"{kernel}/{'work list' if lens else 'grid'}/partition {partition or 'auto'}"
             cache = base.clone()
-            outs[kernel, partition] = ops.decode_attention(q, cache, max_seqlen=max(pos) + 1, seqlens=seqlens,
-                                                           kv_new=kv_new, kernel=kernel, partition=partition)
+            outs[mode] = ops.decode_attention(q, cache, max_seqlen=max(pos) + 1, seqlens=seqlens, kv_new=kv_new,
+                                              kernel=kernel, partition=partition, lens=lens)
             torch.cuda.synchronize()
-            assert np.array_equal(bits(cache), want_cache), f"{kernel}/{partition}: fused append differs"
-            print(f"  {kernel} partition {partition or 'auto'}: append bit-exact", flush=True)
+            assert np.array_equal(bits(cache), want_cache), f"{mode}: fused append differs"
+            print(f"  {mode}: append bit-exact", flush=True)
             del cache
     after = base.clone()
     ops.append_kv(after, kv_new.reshape(B, -1), seqlens)

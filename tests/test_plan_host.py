@@ -1,14 +1,23 @@
-"""Host-side checks of AttendPlan's per-call geometry comparison (no GPU).
+"""Host-side checks (no GPU) of the decode-attention planning code.
 
-An AttendPlan patches only addresses into a parameter block built once, so a
-call with a tensor of another shape, stride, dtype or device, or a short or
-non-contiguous kv_new, must raise ValueError before anything is launched.
-The comparison is a pure function of tensor metadata; it is exercised here on
-CPU tensors."""
+* AttendPlan's per-call geometry comparison: an AttendPlan patches only
+  addresses into a parameter block built once, so a call with a tensor of
+  another shape, stride, dtype or device, or a short or non-contiguous
+  kv_new, must raise ValueError before anything is launched.  The comparison
+  is a pure function of tensor metadata, exercised here on CPU tensors.
+* hexkv_attend_plan (host code of the C library): the work list covers
+  every attended position of every (row, head group) exactly once, the
+  partition numbers and counts agree with the merge's view, the order is
+  empty rows, full chunks, then the shorter last chunks from the longest
+  down, and the library's chunk choice follows its three regimes.
+"""
+import ctypes
+
+import numpy as np
 import pytest
 import torch
 
-from hexgen2_amd import ops
+from hexgen2_amd import _lib, ops
 
 
 def tensors(dtype=torch.bfloat16):
@@ -55,3 +64,123 @@ def test_unfused_plan_rejects_kv_new():
     q, cache, out, kv = tensors()
     with pytest.raises(ValueError, match="kv_new"):
         check((q, cache, out, None), (q, cache, out, kv))
+
+
+# ------------------------------------------------------------ the planner ---
+
+def params(batch, hq, hkv, d, dtype=_lib.HEXKV_BF16, bias=0, max_seqlen=1 << 20, kv_new=True, partition=0):
+    return _lib.AttendParams(dtype=dtype, batch=batch, q_len=1, q_heads=hq, kv_heads=hkv, head_dim=d,
+                             softmax_scale=0.1, seqlen_bias=bias, max_seqlen=max_seqlen,
+                             kv_new=0x1000 if kv_new else None, partition=partition)
+
+
+def plan(p, lens):
+    lib = _lib.load()
+    c_lens = (ctypes.c_int32 * len(lens))(*lens)
+    n, mp = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)),
+               "plan")
+    items = (_lib.WorkItem * max(n.value, 1))()
+    parts = (ctypes.c_int32 * (p.batch * p.q_heads))()
+    n2, mp2 = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, items, n.value, parts, len(parts),
+                                     ctypes.byref(n2), ctypes.byref(mp2)), "plan")
+    assert (n2.value, mp2.value) == (n.value, mp.value)
+    arr = np.array([[it.row, it.head_group, it.part, it.parts, it.first, it.count, it.len, it.reserved]
+                    for it in items[:n.value]], dtype=np.int64)
+    return arr, np.array(parts[:]), mp.value
+
+
+def group_of(hq, hkv):
+    return next(g for g in (8, 4, 2, 1) if (hq // hkv) % g == 0)
+
+
+def check_cover(arr, parts, lens, hq, hkv, bias=0, extra=1):
+    groups = hq // group_of(hq, hkv)
+    att = [n + bias + extra for n in lens]
+    seen = {}
+    for row, hg, part, nparts, first, count, length, _ in arr:
+        assert 0 <= row < len(lens) and 0 <= hg < groups
+        assert length == att[row] and 0 <= first and first + count <= length
+        assert nparts == parts[row * groups + hg] and 0 <= part < nparts
+        seen.setdefault((row, hg), []).append((part, first, count))
+    for row in range(len(lens)):
+        for hg in range(groups):
+            spans = sorted(seen[(row, hg)], key=lambda x: x[1])
+            assert [s[0] for s in spans] == list(range(len(spans))), "partitions numbered in position order"
+            pos = 0
+            for _, first, count in spans:
+                assert first == pos
+                pos += count
+            assert pos == att[row]
+            assert len(spans) == parts[row * groups + hg]
+
+
+@pytest.mark.parametrize("lens,hq,hkv,d", [
+    ([7897, 221, 4000, 1023, 1024, 1025, 0, 5000], 32, 8, 128),   # Llama-3-8B geometry, ragged
+    ([3806, 538, 2000], 8, 1, 128),                                # Llama-2-70B TP-8 share
+    ([512], 32, 4, 64),                                            # TinyLlama: no split
+    ([100, 0, 3], 4, 4, 16),                                       # tiny fp32-style geometry
+])
+def test_plan_covers_every_position_once(lens, hq, hkv, d):
+    p = params(len(lens), hq, hkv, d)
+    arr, parts, max_parts = plan(p, lens)
+    check_cover(arr, parts, lens, hq, hkv)
+    assert max_parts == arr[:, 3].max()
+
+
+def test_plan_order_full_chunks_then_tails_longest_first():
+    lens = [5000, 3000, 2047, 4095]  # +1 attended each (fused append)
+    p = params(len(lens), 32, 8, 128, partition=1024)
+    arr, parts, _ = plan(p, lens)
+    check_cover(arr, parts, lens, 32, 8)
+    counts = arr[:, 5]
+    full = counts == 1024
+    last_full = np.nonzero(full)[0].max()
+    assert full[:last_full + 1].all(), "every full chunk precedes every shorter one"
+    tails = counts[last_full + 1:]
+    assert (np.diff(tails) <= 0).all(), "shorter chunks from the longest down"
+    # chunk index major across segments: the first items are chunk 0 of every segment
+    groups = 32 // 4
+    assert (arr[:len(lens) * groups, 2] == 0).all()
+
+
+def test_plan_empty_rows_come_first_with_zero_counts():
+    lens = [10, 0, 7]
+    p = params(3, 8, 2, 64, kv_new=False)
+    arr, parts, _ = plan(p, lens)
+    check_cover(arr, parts, lens, 8, 2, extra=0)
+    groups = 8 // 4
+    assert (arr[:groups, 0] == 1).all() and (arr[:groups, 5] == 0).all()
+
+
+def test_plan_chunk_regimes():
+    # small call (< 4 MB read): one item per (row, head group), no merge
+    arr, parts, mp = plan(params(1, 32, 4, 64, dtype=_lib.HEXKV_F16), [576])
+    assert mp == 1 and len(arr) == 4
+    # latency-bound (< 64 MB): about 200 items
+    lens = [538 + 37 * i for i in range(32)]
+    arr, _, mp = plan(params(32, 8, 1, 128), lens)
+    assert 150 <= len(arr) <= 300 and mp > 1
+    # bandwidth-bound: 1024-position chunks
+    lens = [8000 - 100 * i for i in range(64)]
+    arr, _, _ = plan(params(64, 32, 8, 128), lens)
+    assert arr[:, 5].max() == 1024
+
+
+def test_plan_rejects_bad_requests():
+    lib = _lib.load()
+    n, mp = ctypes.c_int32(), ctypes.c_int32()
+    lens = (ctypes.c_int32 * 2)(10, 20)
+    p = params(2, 8, 2, 64, max_seqlen=15)  # 20 + 1 keys above max_seqlen
+    assert lib.hexkv_attend_plan(ctypes.byref(p), lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)) \
+        == _lib.HEXKV_ERANGE
+    p = params(2, 8, 2, 64)
+    p.q_len = 2
+    assert lib.hexkv_attend_plan(ctypes.byref(p), lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)) \
+        == _lib.HEXKV_EINVAL
+    p = params(2, 8, 2, 64)
+    items = (_lib.WorkItem * 1)()
+    parts = (ctypes.c_int32 * 16)()
+    assert lib.hexkv_attend_plan(ctypes.byref(p), lens, items, 1, parts, 16, ctypes.byref(n), ctypes.byref(mp)) \
+        == _lib.HEXKV_EINVAL  # room for one item only

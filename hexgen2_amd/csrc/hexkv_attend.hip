@@ -1252,13 +1252,15 @@ namespace hexkv {
 // no merge launch); up to 64 MB it is latency-bound and about 200 items,
 // one per CU, are fastest (the Llama-2-70B TP-8 share: 384-position chunks
 // 13.3 us against 15.2 for the grid, 14.9 at 256, 14.7 at 512); above,
-// 1024-position chunks (Llama-3-8B 170-173 us against 179 for the grid and
-// 179.6 at 512; Llama-2-7B 31.4 against 33.6 for the grid and 34.6 at 1280).
+// 1024-position chunks, or 1280 from a million positions up (Llama-2-7B,
+// 0.34 M positions: 31.4 us at 1024 against 33.6 for the grid and 34.6 at
+// 1280; Llama-3-8B, 2.0 M: 170.3-170.9 us at 1280 against 173.0-173.2 at
+// 1024, 179 for the grid and 179.6 at 512, over three boxes).
 static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest) {
   const int64_t bytes = positions * row_bytes;
   if (bytes < (INT64_C(4) << 20)) return static_cast<int>(std::max<int64_t>(64, (longest + 63) / 64 * 64));
   if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 200 + 63) / 64 * 64)));
-  return 1024;
+  return positions >= (INT64_C(1) << 20) ? 1280 : 1024;
 }
 
 }  // namespace hexkv

@@ -22,7 +22,7 @@ EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "h
            "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
            "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend",
-           "hexkv_attend_noalloc", "hexkv_attend_plan")
+           "hexkv_attend_noalloc", "hexkv_attend_plan", "hexkv_attend_plan_chunk")
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
@@ -115,6 +115,8 @@ def load() -> ctypes.CDLL:
     lib.hexkv_attend_plan.restype = ci
     lib.hexkv_attend_plan.argtypes = [ctypes.POINTER(AttendParams), vp, vp, ctypes.c_int32, vp, ctypes.c_int32,
                                       i32p, i32p]
+    lib.hexkv_attend_plan_chunk.restype = ci
+    lib.hexkv_attend_plan_chunk.argtypes = [ctypes.POINTER(AttendParams), vp, i32p]
     lib.hexkv_attend_noalloc.restype = ci
     lib.hexkv_attend_noalloc.argtypes = [ctypes.POINTER(AttendParams), vp]
     blocks = ctypes.POINTER(Block)

@@ -1138,8 +1138,11 @@ static int validate(const hexkv_attend_params *p) {
   if (p->max_seqlen < 0 || p->max_seqlen > p->capacity)
     return fail(HEXKV_ERANGE, "hexkv_attend: max_seqlen %d outside [0, capacity %lld]",
                 p->max_seqlen, static_cast<long long>(p->capacity));
-  if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > 4096)))
-    return fail(HEXKV_EINVAL, "hexkv_attend: partition must be 0 or a multiple of 64 up to 4096");
+  // With a work list the items carry the positions and the partition is not
+  // read; it may then hold the list's chunk, which can exceed 4096.
+  if (p->partition < 0 || (p->partition > 0 && p->partition % 64 != 0) ||
+      (!p->work_items_dev && p->partition > 4096))
+    return fail(HEXKV_EINVAL, "hexkv_attend: partition must be 0 or a multiple of 64 (up to 4096 without a work list)");
   if (!(p->softmax_scale > 0.f) || p->softmax_scale > 3.0e38f)
     return fail(HEXKV_EINVAL, "hexkv_attend: softmax_scale must be positive and finite");
   if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_MFMA)
@@ -1263,23 +1266,16 @@ static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest) {
   return positions >= (INT64_C(1) << 20) ? 1280 : 1024;
 }
 
-}  // namespace hexkv
-
-extern "C" int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_work_item *items,
-                                 int32_t items_capacity, int32_t *parts, int32_t parts_capacity,
-                                 int32_t *n_items, int32_t *max_parts) {
-  using namespace hexkv;
-  clear_error();
-  const char *what = "hexkv_attend_plan";
-  if (!p || !lens || !n_items || !max_parts) return fail(HEXKV_EINVAL, "%s: null argument", what);
+// Checks a planning request and returns the chunk hexkv_attend_plan cuts
+// segments into (> 0), or a negative error code.
+static int plan_request(const hexkv_attend_params *p, const int32_t *lens, const char *what) {
+  if (!p || !lens) return fail(HEXKV_EINVAL, "%s: null argument", what);
   if (p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads || p->batch < 0 || p->batch > 65535)
     return fail(HEXKV_EINVAL, "%s: bad batch or head counts", what);
   if (p->q_len != 1 || p->causal) return fail(HEXKV_EINVAL, "%s: work lists are for decode rows (q_len 1, not causal)", what);
-  if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > 4096)))
-    return fail(HEXKV_EINVAL, "%s: partition must be 0 or a multiple of 64 up to 4096", what);
-  const int G = kernel_group(p->q_heads / p->kv_heads);
-  const int groups = p->q_heads / G;
-  const int64_t segs = static_cast<int64_t>(p->batch) * groups;
+  if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > (1 << 30))))
+    return fail(HEXKV_EINVAL, "%s: partition must be 0 or a positive multiple of 64", what);
+  const int groups = p->q_heads / kernel_group(p->q_heads / p->kv_heads);
   const int extra = p->kv_new ? 1 : 0;
   int64_t positions = 0, longest = 0;
   for (int b = 0; b < p->batch; ++b) {
@@ -1290,8 +1286,37 @@ extern "C" int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *le
     positions += len * groups;
     longest = std::max(longest, len);
   }
+  if (p->partition > 0) return p->partition;
   const int64_t row_bytes = 2 * static_cast<int64_t>(p->head_dim) * elem_size(p->dtype);
-  const int64_t chunk = p->partition > 0 ? p->partition : plan_chunk(positions, row_bytes, longest);
+  return plan_chunk(positions, row_bytes, longest);
+}
+
+}  // namespace hexkv
+
+extern "C" int hexkv_attend_plan_chunk(const hexkv_attend_params *p, const int32_t *lens, int32_t *chunk) {
+  using namespace hexkv;
+  clear_error();
+  if (!chunk) return fail(HEXKV_EINVAL, "hexkv_attend_plan_chunk: null argument");
+  const int c = plan_request(p, lens, "hexkv_attend_plan_chunk");
+  if (c < 0) return c;
+  *chunk = c;
+  return HEXKV_OK;
+}
+
+extern "C" int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_work_item *items,
+                                 int32_t items_capacity, int32_t *parts, int32_t parts_capacity,
+                                 int32_t *n_items, int32_t *max_parts) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_attend_plan";
+  if (!n_items || !max_parts) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  const int chunk_or_error = plan_request(p, lens, what);
+  if (chunk_or_error < 0) return chunk_or_error;
+  const int64_t chunk = chunk_or_error;
+  const int G = kernel_group(p->q_heads / p->kv_heads);
+  const int groups = p->q_heads / G;
+  const int64_t segs = static_cast<int64_t>(p->batch) * groups;
+  const int extra = p->kv_new ? 1 : 0;
   int64_t count = 0, most = 1, full_rounds = 0;
   for (int b = 0; b < p->batch; ++b) {
     const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;

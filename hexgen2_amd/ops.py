@@ -552,6 +552,19 @@ class AttendPlan:
             self.workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
             self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), need
 
+    def fix_work_list(self, work: WorkList) -> None:
+        """Run every later call on ``work``, whose device buffers the caller
+        refills in place between calls (a captured graph's replays): the
+        per-call list building stops, and the workspace grows to fit
+        ``work.max_parts``."""
+        p = self.params
+        self.lens, self.work_key, self.work = None, None, work
+        work.apply(p)
+        need = int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
+        if need > self.ws_bytes:
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+            self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), need
+
     def check(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
               kv_new: Optional[torch.Tensor]) -> None:
         """Raise ValueError unless the tensors match the plan's geometry."""
@@ -572,6 +585,85 @@ class AttendPlan:
         return out
 
 
+class ReplayWorkLists:
+    """Work lists for a launch captured once and replayed over decode steps.
+
+    Replay k attends ``lens[b] + k + 1`` keys per row (``+ k`` without
+    ``kv_new``).  Every replay's list is cut with one chunk, the library's
+    choice for the last replay the lengths allow (``hexkv_attend_plan_chunk``),
+    so item and partition counts only grow over the replays and the last
+    replay's sizes -- the captured grid and workspace -- bound them all.
+    ``load(k)`` plans replay k on the host, pads the list to the captured
+    item count with items the kernels skip (row = batch, outside the call),
+    and copies it to fixed device buffers on the current stream; the host
+    buffers alternate, and one is rewritten only after its previous copy has
+    run.
+    """
+
+    def __init__(self, p: _lib.AttendParams, lens: Sequence[int], max_seqlen: int, device):
+        self.lib = _lib.load()
+        if len(lens) != p.batch:
+            raise ValueError(f"{len(lens)} host lengths for a batch of {p.batch}")
+        self.lens = [int(n) for n in lens]
+        self.extra = 1 if p.kv_new else 0
+        self.replays = int(max_seqlen) - max(self.lens, default=0) - self.extra + 1
+        if self.replays < 1:
+            raise ValueError(f"max_seqlen {max_seqlen} leaves no replay for lengths up to {max(self.lens)}")
+        self.params = _lib.AttendParams.from_buffer_copy(p)
+        q = self.params
+        q.max_seqlen, q.work_items_dev, q.work_parts_dev = int(max_seqlen), None, None
+        self.c_lens = (ctypes.c_int32 * len(self.lens))(*self.lens)
+        q.seqlen_bias = self.replays - 1
+        chunk = ctypes.c_int32()
+        _lib.check(self.lib.hexkv_attend_plan_chunk(ctypes.byref(q), self.c_lens, ctypes.byref(chunk)),
+                   "hexkv_attend_plan_chunk")
+        q.partition = chunk.value
+        n, mp = ctypes.c_int32(), ctypes.c_int32()
+        _lib.check(self.lib.hexkv_attend_plan(ctypes.byref(q), self.c_lens, None, 0, None, 0, ctypes.byref(n),
+                                              ctypes.byref(mp)), "hexkv_attend_plan")
+        self.chunk, self.capacity, self.max_parts = chunk.value, max(n.value, 1), mp.value
+        self.n_segs = max(p.batch * p.q_heads, 1)  # head groups never outnumber query heads
+        words = self.capacity * 8 + self.n_segs  # the items, then the partition counts
+        self.host = [torch.empty(words, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self.copied = [torch.cuda.Event(), torch.cuda.Event()]
+        self.pending = [False, False]
+        self.dev = torch.empty(words, dtype=torch.int32, device=device)
+        self.work = WorkList(self.dev[:self.capacity * 8].view(self.capacity, 8), self.dev[self.capacity * 8:],
+                             self.capacity, self.max_parts)
+        for buf in self.host:
+            self._pad(buf, 0)
+        self.filled = [0, 0]  # items the last plan wrote into each host buffer
+        self.dev.copy_(self.host[0])
+
+    def _pad(self, buf: torch.Tensor, n: int) -> None:
+        items = buf[:self.capacity * 8].view(self.capacity, 8)
+        items[n:] = 0
+        items[n:, 0] = self.params.batch
+
+    def load(self, k: int) -> None:
+        if not 0 <= k < self.replays:
+            raise RuntimeError(f"work lists built for replays 0..{self.replays - 1}, asked for {k}")
+        i = k % 2
+        if self.pending[i]:
+            self.copied[i].synchronize()
+        buf = self.host[i]
+        q = self.params
+        q.seqlen_bias = k
+        n, mp = ctypes.c_int32(), ctypes.c_int32()
+        base = buf.data_ptr()
+        _lib.check(self.lib.hexkv_attend_plan(ctypes.byref(q), self.c_lens, ctypes.c_void_p(base), self.capacity,
+                                              ctypes.c_void_p(base + self.capacity * 32), self.n_segs,
+                                              ctypes.byref(n), ctypes.byref(mp)), "hexkv_attend_plan")
+        if mp.value > self.max_parts:
+            raise RuntimeError(f"replay {k} needs {mp.value} partitions, {self.max_parts} captured")
+        if n.value < self.filled[i]:  # counts only grow over replays; kept for any caller
+            self._pad(buf, n.value)
+        self.filled[i] = n.value
+        self.dev.copy_(buf, non_blocking=True)
+        self.copied[i].record()
+        self.pending[i] = True
+
+
 class DecodeStepGraph:
     """One decode step's fused append + attend over every layer, captured once
     as a HIP graph and replayed per step.
@@ -585,6 +677,16 @@ class DecodeStepGraph:
     This is the graph-captured decode step of hexgen_core's generation loop
     (hexgen/hexgen_core/generation.py:354-443) restricted to the KV path.
 
+    ``lens``, the host values of ``positions`` at the first replay, switches
+    the attention to work lists (``ReplayWorkLists``): each replay first
+    plans its step on the host and copies the list to the buffers the graph
+    reads, then launches the graph.  Replay k then attends ``lens + k + 1``
+    keys whatever ``positions`` holds (which still advances by one per
+    replay), and ``max_seqlen`` should be tight: the captured grid is the
+    item count of the last replay it allows.  ``step`` counts the replays.
+    ``partition`` sets the positions per partition (grid) or per item (work
+    list); 0 leaves it to the library.
+
     The kernels must have run once eagerly in this process before capture
     (code objects load on first launch).  Graph nodes hold the tensors'
     addresses: the tensors must stay alive, and be updated in place, for as
@@ -593,7 +695,8 @@ class DecodeStepGraph:
 
     def __init__(self, q_layers: TensorList, cache_layers: TensorList, out_layers: TensorList,
                  kv_new_layers: TensorList, positions: torch.Tensor, max_seqlen: int,
-                 softmax_scale: Optional[float] = None, kernel: str = "auto"):
+                 softmax_scale: Optional[float] = None, kernel: str = "auto",
+                 lens: Optional[Sequence[int]] = None, partition: int = 0):
         self.q, self.cache = _as_layers(q_layers), _as_layers(cache_layers)
         self.out, self.kv_new = _as_layers(out_layers), _as_layers(kv_new_layers)
         if not (len(self.q) == len(self.cache) == len(self.out) == len(self.kv_new)) or not self.q:
@@ -604,10 +707,15 @@ class DecodeStepGraph:
         self.positions, self.max_seqlen = positions, int(max_seqlen)
         self.plan = AttendPlan(self.q[0], self.cache[0], self.out[0], max_seqlens=[self.max_seqlen],
                                seqlens=positions, kv_new=self.kv_new[0], softmax_scale=softmax_scale,
-                               kernel=kernel)
+                               kernel=kernel, partition=partition)
         # Every layer is checked before anything is captured.
         for l in range(len(self.q)):
             self.plan.check(self.q[l], self.cache[l], self.out[l], self.kv_new[l])
+        self.lists = None
+        if lens is not None:
+            self.lists = ReplayWorkLists(self.plan.params, lens, self.max_seqlen, positions.device)
+            self.plan.fix_work_list(self.lists.work)
+        self.step = 0
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             for l in range(len(self.q)):
@@ -615,7 +723,15 @@ class DecodeStepGraph:
             self.positions.add_(1)
 
     def replay(self) -> None:
+        if self.lists is not None:
+            self.lists.load(self.step)
         self.graph.replay()
+        self.step += 1
+
+    def restart(self) -> None:
+        """Make the next replay replay 0 again (a new decode over the same
+        lengths); the caller restores ``positions`` and the caches."""
+        self.step = 0
 
 
 class FtDecodeStepGraph:

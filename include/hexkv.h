@@ -230,7 +230,8 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
  * row b attends len_b = lens[b] + p->seqlen_bias (+1 with kv_new) keys,
  * each within [0, p->max_seqlen].  Every (row, head group) segment is cut
  * into chunks of p->partition positions (0: the library's choice by the
- * bytes the call reads), and the items are ordered for the launch: empty
+ * bytes the call reads, see hexkv_attend_plan_chunk; else a multiple of 64),
+ * and the items are ordered for the launch: empty
  * rows, then the full chunks across all segments, then each segment's last,
  * shorter chunk from the longest down.  Host memory only; the caller copies
  * `items` and `parts` to the device and passes them in
@@ -250,6 +251,19 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
 int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_work_item *items,
                       int32_t items_capacity, int32_t *parts, int32_t parts_capacity,
                       int32_t *n_items, int32_t *max_parts);
+
+/*
+ * The chunk (positions per work item) hexkv_attend_plan uses for these
+ * lengths: p->partition when set, else the library's choice -- one chunk per
+ * segment below 4 MB read, about 200 items below 64 MB, 1024 positions
+ * above (1280 from 2^20 positions up).  A caller that replays one captured
+ * launch over several steps plans every step with the chunk of its last
+ * (longest) step, passed as p->partition, so the item and partition counts
+ * only grow and the last step's sizes bound every step.  Returns HEXKV_OK
+ * with *chunk set, or an error as hexkv_attend_plan.  No counterpart in the
+ * reference (it has no planning step).
+ */
+int hexkv_attend_plan_chunk(const hexkv_attend_params *p, const int32_t *lens, int32_t *chunk);
 
 /* Size of the static scratch array behind hexkv_attend_noalloc (per GPU). */
 #define HEXKV_NOALLOC_SCRATCH_BYTES (32u << 20)

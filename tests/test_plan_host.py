@@ -187,3 +187,50 @@ def test_plan_rejects_bad_requests():
     parts = (ctypes.c_int32 * 16)()
     assert lib.hexkv_attend_plan(ctypes.byref(p), lens, items, 1, parts, 16, ctypes.byref(n), ctypes.byref(mp)) \
         == _lib.HEXKV_EINVAL  # room for one item only
+
+
+def plan_chunk(p, lens):
+    lib = _lib.load()
+    c_lens = (ctypes.c_int32 * len(lens))(*lens)
+    chunk = ctypes.c_int32()
+    rc = lib.hexkv_attend_plan_chunk(ctypes.byref(p), c_lens, ctypes.byref(chunk))
+    return rc, chunk.value
+
+
+@pytest.mark.parametrize("lens,hq,hkv,d,dtype", [
+    ([576], 32, 4, 64, _lib.HEXKV_F16),                          # one chunk per segment
+    ([538 + 37 * i for i in range(32)], 8, 1, 128, _lib.HEXKV_BF16),  # about 200 items
+    ([2000 - 10 * i for i in range(64)], 32, 8, 128, _lib.HEXKV_BF16),
+    ([8000 - 100 * i for i in range(64)], 32, 8, 128, _lib.HEXKV_BF16),
+])
+def test_plan_chunk_is_the_planners_chunk(lens, hq, hkv, d, dtype):
+    """hexkv_attend_plan_chunk names the chunk the planner cuts with: no item
+    is longer, every item but a segment's last has exactly that length, and
+    planning with it passed as the partition gives the same list."""
+    p = params(len(lens), hq, hkv, d, dtype=dtype)
+    rc, chunk = plan_chunk(p, lens)
+    assert rc == 0 and chunk > 0 and chunk % 64 == 0
+    arr, parts, mp = plan(p, lens)
+    assert arr[:, 5].max() <= chunk
+    not_last = arr[:, 2] < arr[:, 3] - 1
+    assert (arr[not_last, 5] == chunk).all()
+    p2 = params(len(lens), hq, hkv, d, dtype=dtype, partition=chunk)
+    arr2, parts2, mp2 = plan(p2, lens)
+    assert np.array_equal(arr, arr2) and np.array_equal(parts, parts2) and mp == mp2
+    assert plan_chunk(p2, lens) == (0, chunk)
+
+
+def test_plan_takes_chunks_beyond_4096():
+    """A work list may use chunks above the grid's 4096-position cap (the
+    one-chunk-per-segment regime reaches them); the planner takes any
+    positive multiple of 64."""
+    lens = [9000, 100]
+    p = params(2, 8, 2, 64, partition=8192)
+    arr, parts, mp = plan(p, lens)
+    check_cover(arr, parts, lens, 8, 2)
+    assert mp == 2 and arr[:, 5].max() == 8192
+    for bad in (100, -64):
+        rc, _ = plan_chunk(params(2, 8, 2, 64, partition=bad), lens)
+        assert rc == _lib.HEXKV_EINVAL
+    rc, _ = plan_chunk(params(2, 8, 2, 64, max_seqlen=50), lens)
+    assert rc == _lib.HEXKV_ERANGE

@@ -61,6 +61,64 @@ struct SpanArgs {
 };
 static_assert(sizeof(SpanArgs) <= 4096, "kernel arguments above 4 KiB");
 
+// The work of one span_copy_kernel workgroup (`tile`): rows [r0, r1) of
+// one slice of one layer of one span, `bytes` of each row from column c0.
+// Host and device share this decode (the CPU emulation of the kernel calls
+// it), so the arithmetic that is bounds-checked is the one that runs.
+struct SpanTile {
+  const char *src;  // the tile's first byte in row 0 (nullptr: zero fill)
+  char *dst;
+  int64_t src_row, dst_row;  // row pitches, bytes
+  int64_t bytes;             // bytes of each row this tile moves
+  int r0, r1;
+};
+
+__host__ __device__ inline int span_of_tile(const SpanArgs &a, int tile) {
+  int lo = 0, hi = a.n;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (a.first_tile[mid] <= tile) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+__host__ __device__ inline SpanTile span_tile(const SpanArgs &a, int tile) {
+  const int i = span_of_tile(a, tile);
+  const Span &s = a.span[i];
+  int t = tile - a.first_tile[i];
+  const int ct = t % s.col_tiles;
+  t /= s.col_tiles;
+  const int rt = t % s.row_tiles;
+  t /= s.row_tiles;
+  const int64_t k = t % s.depth;  // slice
+  const int64_t m = t / s.depth;  // layer
+  const int64_t c0 = static_cast<int64_t>(ct) * s.tile_cols;
+  const int64_t c1 = s.width < c0 + s.tile_cols ? s.width : c0 + s.tile_cols;
+  SpanTile w;
+  w.src = s.src ? s.src + m * s.src_layer + k * s.src_slice + c0 : nullptr;
+  w.dst = s.dst + m * s.dst_layer + k * s.dst_slice + c0;
+  w.src_row = s.src_row;
+  w.dst_row = s.dst_row;
+  w.bytes = c1 - c0;
+  w.r0 = rt * s.tile_rows;
+  w.r1 = s.height < w.r0 + s.tile_rows ? s.height : w.r0 + s.tile_rows;
+  return w;
+}
+
+// Short rows (fewer vectors than threads): `per` rows per pass, lane `tid`
+// at (row in pass tr, vector tc); lanes with tr >= per idle.
+struct RowLane {
+  int per, tr, tc;
+};
+
+__host__ __device__ inline RowLane row_lane(int threads, int vectors, int tid) {
+  RowLane l;
+  l.per = threads / vectors;
+  l.tr = tid / vectors;
+  l.tc = tid - l.tr * vectors;
+  return l;
+}
+
 // A wide row piece: the workgroup strides along it.  A zero fill (no
 // source) has its own loop with eight stores in flight per lane: on MI355X
 // zero-pad batching moved 5.12 TB/s with it against 5.05 with the copy loop
@@ -92,49 +150,28 @@ __device__ __forceinline__ void move_row(const char *__restrict__ s, char *__res
 
 template <typename V, int T, int UR>
 __global__ __launch_bounds__(T) void span_copy_kernel(const SpanArgs a) {
-  const int tile = blockIdx.x;
-  int lo = 0, hi = a.n;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (a.first_tile[mid] <= tile) lo = mid; else hi = mid;
-  }
-  const Span &s = a.span[lo];
-  int t = tile - a.first_tile[lo];
-  const int ct = t % s.col_tiles;
-  t /= s.col_tiles;
-  const int rt = t % s.row_tiles;
-  t /= s.row_tiles;
-  const int64_t k = t % s.depth;  // slice
-  const int64_t m = t / s.depth;  // layer
-  const int r0 = rt * s.tile_rows;
-  const int r1 = min(s.height, r0 + s.tile_rows);
-  const int64_t c0 = static_cast<int64_t>(ct) * s.tile_cols;
-  const int64_t nv = (min(s.width, c0 + s.tile_cols) - c0) / static_cast<int64_t>(sizeof(V));
-  const char *src = s.src ? s.src + m * s.src_layer + k * s.src_slice + c0 : nullptr;
-  char *dst = s.dst + m * s.dst_layer + k * s.dst_slice + c0;
+  const SpanTile w = span_tile(a, blockIdx.x);
+  const int64_t nv = w.bytes / static_cast<int64_t>(sizeof(V));
   if (nv >= T) {
-    for (int r = r0; r < r1; ++r)
-      move_row<V, T, UR>(src ? src + r * s.src_row : nullptr, dst + r * s.dst_row, nv);
+    for (int r = w.r0; r < w.r1; ++r)
+      move_row<V, T, UR>(w.src ? w.src + r * w.src_row : nullptr, w.dst + r * w.dst_row, nv);
     return;
   }
-  // Short rows: `per` rows per pass, lane (tr, tc) = (row in pass, vector).
-  const int per = T / static_cast<int>(nv);
-  const int tr = threadIdx.x / static_cast<int>(nv);
-  const int tc = threadIdx.x - tr * static_cast<int>(nv);
-  if (tr >= per) return;
-  const int64_t col = static_cast<int64_t>(tc) * static_cast<int64_t>(sizeof(V));
-  for (int r = r0 + tr; r < r1; r += per * UR) {
+  const RowLane l = row_lane(T, static_cast<int>(nv), threadIdx.x);
+  if (l.tr >= l.per) return;
+  const int64_t col = static_cast<int64_t>(l.tc) * static_cast<int64_t>(sizeof(V));
+  for (int r = w.r0 + l.tr; r < w.r1; r += l.per * UR) {
     V v[UR];
 #pragma unroll
     for (int u = 0; u < UR; ++u) {
-      const int rr = r + u * per;
+      const int rr = r + u * l.per;
       v[u] = V{};
-      if (src && rr < r1) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V *>(src + rr * s.src_row + col));
+      if (w.src && rr < w.r1) v[u] = __builtin_nontemporal_load(reinterpret_cast<const V *>(w.src + rr * w.src_row + col));
     }
 #pragma unroll
     for (int u = 0; u < UR; ++u) {
-      const int rr = r + u * per;
-      if (rr < r1) __builtin_nontemporal_store(v[u], reinterpret_cast<V *>(dst + rr * s.dst_row + col));
+      const int rr = r + u * l.per;
+      if (rr < w.r1) __builtin_nontemporal_store(v[u], reinterpret_cast<V *>(w.dst + rr * w.dst_row + col));
     }
   }
 }
@@ -161,29 +198,54 @@ struct GatherArgs {
   int32_t rows_per_tile;
 };
 
-__global__ __launch_bounds__(kWideThreads) void head_gather_kernel(const GatherArgs a) {
-  const int64_t l = blockIdx.y;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_tile;
-  const int64_t r1 = min(a.rows, r0 + a.rows_per_tile);
-  const int per = kWideThreads / a.wvec;  // destination rows per pass
-  const int tr = threadIdx.x / a.wvec, tc = threadIdx.x - tr * a.wvec;
-  if (tr >= per) return;
+// What lane `tid` of head_gather_kernel's workgroup (tile, layer) moves:
+// destination rows r0 + tr, r0 + tr + per, ... below r1, 16 bytes at column
+// vector tc, read from shard `shard`.  Shared with the CPU emulation.
+struct GatherLane {
+  const char *src;  // the lane's 16 bytes in source row 0
+  char *dst;        // the lane's 16 bytes in destination row 0
+  int64_t src_pitch, dst_pitch, r0, r1;
+  int per, tr, tc, shard;
+};
+
+__host__ __device__ inline GatherLane gather_lane(const GatherArgs &a, int64_t tile, int64_t layer, int tid) {
+  GatherLane g;
+  const RowLane rl = row_lane(kWideThreads, a.wvec, tid);
+  g.per = rl.per;
+  g.tr = rl.tr;
+  g.tc = rl.tc;
+  g.r0 = tile * a.rows_per_tile;
+  g.r1 = a.rows < g.r0 + a.rows_per_tile ? a.rows : g.r0 + a.rows_per_tile;
   int j = 0;
-  while (j + 1 < a.n && a.vec_start[j + 1] <= tc) ++j;
-  const char *src = a.src[j] + l * a.src_layer[j] + static_cast<int64_t>(tc - a.vec_start[j]) * 16;
-  const int64_t sp = a.src_pitch[j], dp = static_cast<int64_t>(a.wvec) * 16;
-  char *dst = a.dst + l * a.dst_layer + static_cast<int64_t>(tc) * 16;
-  for (int64_t r = r0 + tr; r < r1; r += static_cast<int64_t>(per) * kWideUnroll) {
+  while (j + 1 < a.n && a.vec_start[j + 1] <= g.tc) ++j;
+  g.shard = j;
+  g.src = a.src[j] + layer * a.src_layer[j] + static_cast<int64_t>(g.tc - a.vec_start[j]) * 16;
+  g.src_pitch = a.src_pitch[j];
+  g.dst = a.dst + layer * a.dst_layer + static_cast<int64_t>(g.tc) * 16;
+  g.dst_pitch = static_cast<int64_t>(a.wvec) * 16;
+  return g;
+}
+
+// The row lane u of a pass starting at row r loads: past the tile's last
+// row it reloads that row (a clamped, in-bounds load whose value is not
+// stored), so every lane issues kWideUnroll loads before any store.
+__host__ __device__ inline int64_t gather_load_row(const GatherLane &g, int64_t r, int u) {
+  const int64_t rr = r + static_cast<int64_t>(u) * g.per;
+  return rr < g.r1 - 1 ? rr : g.r1 - 1;
+}
+
+__global__ __launch_bounds__(kWideThreads) void head_gather_kernel(const GatherArgs a) {
+  const GatherLane g = gather_lane(a, blockIdx.x, blockIdx.y, threadIdx.x);
+  if (g.tr >= g.per) return;
+  for (int64_t r = g.r0 + g.tr; r < g.r1; r += static_cast<int64_t>(g.per) * kWideUnroll) {
     u32x4 v[kWideUnroll];
 #pragma unroll
-    for (int u = 0; u < kWideUnroll; ++u) {
-      const int64_t rr = min(r + u * per, r1 - 1);
-      v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + rr * sp));
-    }
+    for (int u = 0; u < kWideUnroll; ++u)
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(g.src + gather_load_row(g, r, u) * g.src_pitch));
 #pragma unroll
     for (int u = 0; u < kWideUnroll; ++u) {
-      const int64_t rr = r + u * per;
-      if (rr < r1) __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4 *>(dst + rr * dp));
+      const int64_t rr = r + u * g.per;
+      if (rr < g.r1) __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4 *>(g.dst + rr * g.dst_pitch));
     }
   }
 }

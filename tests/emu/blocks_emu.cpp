@@ -2,8 +2,9 @@
 // shapes, head_gather_kernel) for bounds and correctness checks without a
 // GPU.  The real host code of hexkv_blocks.hip is compiled in; its kernel
 // launches are intercepted (hipLaunchKernel and the call-configuration hooks
-// are defined here) and each workgroup and lane is replayed on the CPU with
-// the kernel's own index arithmetic.  Every source and destination access
+// are defined here) and each workgroup and lane is replayed on the CPU
+// through the kernels' own __host__ __device__ index functions (span_tile,
+// row_lane, gather_lane, gather_load_row).  Every source and destination access
 // must fall inside a registered buffer and be aligned to its vector width;
 // the bytes are moved, so the caller can compare the result with the
 // oracle.  Used by tests/test_blocks_emulated.py.
@@ -35,62 +36,56 @@ static void move(const char *s, char *d, size_t vs) {
   if (s) memcpy(d, s, vs); else memset(d, 0, vs);
 }
 
+// span_copy_kernel, workgroup by workgroup and lane by lane: the tile decode
+// (span_tile) and the short-row lane mapping (row_lane) are the kernel's
+// own functions; the loops visit the rows and vectors the kernel's loops do.
 static void emulate(const hexkv::SpanArgs &a, unsigned grid, size_t vs, int T) {
   using namespace hexkv;
   for (unsigned tile = 0; tile < grid; ++tile) {
-    int lo = 0, hi = a.n;
-    while (hi - lo > 1) { int mid = (lo + hi) >> 1; if (a.first_tile[mid] <= (int)tile) lo = mid; else hi = mid; }
-    const Span &s = a.span[lo];
-    int t = tile - a.first_tile[lo];
-    if (t < 0 || t >= a.first_tile[lo + 1] - a.first_tile[lo]) { g_violations++; fprintf(stderr, "tile map\n"); }
-    const int ct = t % s.col_tiles; t /= s.col_tiles;
-    const int rt = t % s.row_tiles; t /= s.row_tiles;
-    const int64_t k = t % s.depth, m = t / s.depth;
-    const int r0 = rt * s.tile_rows, r1 = std::min(s.height, r0 + s.tile_rows);
-    const int64_t c0 = (int64_t)ct * s.tile_cols;
-    const int64_t nv = (std::min(s.width, c0 + s.tile_cols) - c0) / (int64_t)vs;
-    const char *src = s.src ? s.src + m * s.src_layer + k * s.src_slice + c0 : nullptr;
-    char *dst = s.dst + m * s.dst_layer + k * s.dst_slice + c0;
+    const int i = span_of_tile(a, (int)tile);
+    const int t = (int)tile - a.first_tile[i];
+    if (i < 0 || i >= a.n || t < 0 || t >= a.first_tile[i + 1] - a.first_tile[i]) {
+      g_violations++;
+      fprintf(stderr, "tile map\n");
+      continue;
+    }
+    const SpanTile w = span_tile(a, (int)tile);
+    const int64_t nv = w.bytes / (int64_t)vs;
+    if (w.bytes % (int64_t)vs || nv < 1) { g_violations++; fprintf(stderr, "tile width %lld\n", (long long)w.bytes); }
     g_tiles++;
     for (int tid = 0; tid < T; ++tid) {
       if (nv >= T) {
-        for (int r = r0; r < r1; ++r)
-          for (int64_t i = tid; i < nv; i += T)
-            move(src ? src + r * s.src_row + i * vs : nullptr, dst + r * s.dst_row + i * vs, vs);
+        for (int r = w.r0; r < w.r1; ++r)
+          for (int64_t v = tid; v < nv; v += T)
+            move(w.src ? w.src + r * w.src_row + v * vs : nullptr, w.dst + r * w.dst_row + v * vs, vs);
       } else {
-        const int per = T / (int)nv, tr = tid / (int)nv, tc = tid - tr * (int)nv;
-        if (tr >= per) continue;
-        for (int r = r0 + tr; r < r1; r += per)
-          move(src ? src + r * s.src_row + tc * vs : nullptr, dst + r * s.dst_row + tc * vs, vs);
+        const RowLane l = row_lane(T, (int)nv, tid);
+        if (l.tr >= l.per) continue;
+        for (int r = w.r0 + l.tr; r < w.r1; r += l.per)
+          move(w.src ? w.src + r * w.src_row + l.tc * vs : nullptr, w.dst + r * w.dst_row + l.tc * vs, vs);
       }
     }
   }
 }
 
-// head_gather_kernel, lane by lane, with the kernel's own index arithmetic
-// (clamped loads included: every load address is checked).
+// head_gather_kernel, lane by lane, through the kernel's own gather_lane and
+// gather_load_row (clamped loads included: every load address is checked).
 static void emulate_gather(const hexkv::GatherArgs &a, dim3 grid) {
   using namespace hexkv;
   if (a.wvec < 1 || a.wvec > kWideThreads || a.n < 1 || a.n > kGatherShards) { g_violations++; fprintf(stderr, "gather args\n"); return; }
   for (unsigned ly = 0; ly < grid.y; ++ly)
     for (unsigned bx = 0; bx < grid.x; ++bx) {
       g_tiles++;
-      const int64_t l = ly, r0 = (int64_t)bx * a.rows_per_tile, r1 = std::min(a.rows, r0 + a.rows_per_tile);
-      const int per = kWideThreads / a.wvec;
       for (int tid = 0; tid < kWideThreads; ++tid) {
-        const int tr = tid / a.wvec, tc = tid - tr * a.wvec;
-        if (tr >= per) continue;
-        int j = 0;
-        while (j + 1 < a.n && a.vec_start[j + 1] <= tc) ++j;
-        if (tc < a.vec_start[j] || tc >= a.vec_start[j + 1]) { g_violations++; fprintf(stderr, "shard map\n"); continue; }
-        const char *src = a.src[j] + l * a.src_layer[j] + (int64_t)(tc - a.vec_start[j]) * 16;
-        const int64_t sp = a.src_pitch[j], dp = (int64_t)a.wvec * 16;
-        char *dst = a.dst + l * a.dst_layer + (int64_t)tc * 16;
-        for (int64_t r = r0 + tr; r < r1; r += (int64_t)per * kWideUnroll)
+        const GatherLane g = gather_lane(a, bx, ly, tid);
+        if (g.tr >= g.per) continue;
+        if (g.tc < a.vec_start[g.shard] || g.tc >= a.vec_start[g.shard + 1]) { g_violations++; fprintf(stderr, "shard map\n"); continue; }
+        for (int64_t r = g.r0 + g.tr; r < g.r1; r += (int64_t)g.per * kWideUnroll)
           for (int u = 0; u < kWideUnroll; ++u) {
-            const int64_t rr = std::min(r + u * per, r1 - 1);
-            if (!inside((uintptr_t)(src + rr * sp), 16, false)) { if (g_violations++ < 10) fprintf(stderr, "gather load OOB\n"); }
-            if (r + u * per < r1) move(src + (r + u * per) * sp, dst + (r + u * per) * dp, 16);
+            const int64_t lr = gather_load_row(g, r, u);
+            if (!inside((uintptr_t)(g.src + lr * g.src_pitch), 16, false)) { if (g_violations++ < 10) fprintf(stderr, "gather load OOB\n"); }
+            const int64_t rr = r + (int64_t)u * g.per;
+            if (rr < g.r1) move(g.src + rr * g.src_pitch, g.dst + rr * g.dst_pitch, 16);
           }
       }
     }

@@ -1,6 +1,7 @@
 """Seeded random-shape parity sweeps on the GPU: many small configurations
 of the pack/unpack round trip, the fused append + attention (both kernels,
-forced partitions) and the FT decode step, each against the oracle.  The
+forced partitions), attention over host-planned work lists and the FT
+decode step, each against the oracle.  The
 seeds are fixed, so every run checks the same cases."""
 import numpy as np
 import pytest
@@ -75,6 +76,52 @@ def test_random_fused_attention(device, seed):
     ref = oracle.attend(f64(q), f64(cache), [n + 1 for n in lens])
     err = np.abs(f64(out) - ref).max()
     assert err <= TOL[dtype], f"max-abs error {err}"
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_work_list_attention(device, seed):
+    """Attention over host-planned work lists (hexkv_attend_plan) on random
+    shapes: chunk sizes from 64 positions to beyond the grid's 4096 cap,
+    a length bias, with and without the fused append (empty rows then give
+    zero outputs)."""
+    rng = np.random.default_rng(4000 + seed)
+    dtype, hkv, group, d, batch, lens = draw(rng)
+    hq = hkv * group
+    kernel = "mfma" if dtype != torch.float32 and d >= 64 and rng.integers(2) else "valu"
+    partition = int(rng.choice([0, 64, 128, 320, 512, 4160]))
+    fused = bool(rng.integers(2))
+    bias = int(rng.integers(0, 4))
+    if seed % 4 == 0:  # an empty row: no append, no bias
+        fused, bias, lens[0] = False, 0, 0
+    extra = 1 if fused else 0
+    attended = [n + bias + extra for n in lens]
+    cap = max(lens) + bias + 2
+    print(f"fuzz list seed={seed} {dtype} B={batch} hq={hq} hkv={hkv} d={d} {kernel} part={partition} "
+          f"fused={fused} bias={bias} lens={lens}", flush=True)
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn((batch, 1, hq, d), generator=g, device=device).to(dtype)
+    cache = torch.randn((batch, cap, 2, hkv, d), generator=g, device=device).to(dtype)
+    kv_new = torch.randn((batch, 2, hkv, d), generator=g, device=device).to(dtype) if fused else None
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    before = bits(cache)
+    out = torch.full_like(q, 7.0)
+    ops.decode_attention(q, cache, max_seqlen=max(attended), seqlens=seqlens, seqlen_bias=bias,
+                         kv_new=kv_new, out=out, partition=partition, kernel=kernel, lens=lens)
+    torch.cuda.synchronize()
+    if fused:
+        appended = oracle.append(before, bits(kv_new).reshape(batch, -1), [n + bias for n in lens])
+        np.testing.assert_array_equal(bits(cache), appended)
+    else:
+        np.testing.assert_array_equal(bits(cache), before)
+    got = f64(out)
+    live = [b for b in range(batch) if attended[b] > 0]
+    for b in range(batch):
+        if attended[b] == 0:
+            assert not got[b].any(), f"empty row {b} not zero"
+    if live:
+        ref = oracle.attend(f64(q)[live], f64(cache)[live], [attended[b] for b in live])
+        err = np.abs(got[live] - ref).max()
+        assert err <= TOL[dtype], f"max-abs error {err}"
 
 
 @pytest.mark.parametrize("seed", range(16))

@@ -1,8 +1,9 @@
 """hexkv_attend_noalloc (static per-GPU scratch, no allocation) against
 hexkv_attend (caller's workspace), both called through the C ABI.
 
-The two entry points run the same kernels with the same partitioning, so
-their outputs must agree bit for bit (and the fused append must write the
+The two entry points run the same kernels with the same partitioning (the
+library's grid, or one host-planned work list for both), so their outputs
+must agree bit for bit (and the fused append must write the
 same cache bytes); each output is also checked against the float64 oracle
 (bf16 8e-3, fp16 2e-3 max-abs).  Two calls in a row, the second with fewer
 rows and shorter lengths, so stale partials of the first call in the shared
@@ -31,39 +32,47 @@ def stream_of(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def both(q, cache, lens, kv_new, kernel):
-    """(workspace output, no-alloc output, cache after each) of one call."""
+def both(q, cache, lens, kv_new, kernel, listed=False):
+    """(workspace output, no-alloc output, cache after each) of one call;
+    ``listed``: both calls run the same host-planned work list (its device
+    buffers are the caller's inputs)."""
     lib = _lib.load()
     seqlens = torch.tensor(lens, dtype=torch.int32, device=q.device)
     max_seqlen = max(lens) + 1
     c_ws, c_na = cache.clone(), cache.clone()
     o_ws, o_na = torch.full_like(q, 7.0), torch.full_like(q, -7.0)
     p = ops._attend_params(q, c_ws, o_ws, seqlens, 0, max_seqlen, kv_new, False, None, 0, kernel)
+    work = ops._plan_work(p, lens, q.device) if listed else None
+    if work:
+        work.apply(p)
     need = lib.hexkv_attend_workspace_bytes(ctypes.byref(p))
     assert 0 < need <= _lib.NOALLOC_SCRATCH_BYTES
     ws = torch.empty(need, dtype=torch.uint8, device=q.device)
     _lib.check(lib.hexkv_attend(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need, stream_of(q)),
                "hexkv_attend")
     p = ops._attend_params(q, c_na, o_na, seqlens, 0, max_seqlen, kv_new, False, None, 0, kernel)
+    if work:
+        work.apply(p)
     _lib.check(lib.hexkv_attend_noalloc(ctypes.byref(p), stream_of(q)), "hexkv_attend_noalloc")
     torch.cuda.synchronize()
     return o_ws, o_na, c_ws, c_na
 
 
+@pytest.mark.parametrize("listed", [False, True], ids=["grid", "work_list"])
 @pytest.mark.parametrize("dtype,hq,hkv,d,kernel", [(torch.bfloat16, 32, 8, 128, "valu"),
                                                    (torch.bfloat16, 8, 1, 128, "mfma"),
                                                    (torch.float16, 32, 4, 64, "mfma")])
-def test_noalloc_matches_workspace_entry_point(device, dtype, hq, hkv, d, kernel):
+def test_noalloc_matches_workspace_entry_point(device, dtype, hq, hkv, d, kernel, listed):
     g = torch.Generator(device=device).manual_seed(31)
     calls = [[5000, 17, 3000, 1, 2048, 700, 4095, 64, 1500, 333, 2600, 4000],  # up to 40 partitions
              [900, 3, 650]]                                                   # second call: smaller
     for i, lens in enumerate(calls):
-        print(f"noalloc {dtype} {hq}/{hkv}/{d} {kernel} call {i}: {len(lens)} rows", flush=True)
+        print(f"noalloc {dtype} {hq}/{hkv}/{d} {kernel} list={listed} call {i}: {len(lens)} rows", flush=True)
         cap = max(lens) + 8
         q = torch.randn((len(lens), 1, hq, d), generator=g, device=device).to(dtype)
         cache = torch.randn((len(lens), cap, 2, hkv, d), generator=g, device=device).to(dtype)
         kv_new = torch.randn((len(lens), 2, hkv, d), generator=g, device=device).to(dtype)
-        o_ws, o_na, c_ws, c_na = both(q, cache, lens, kv_new, kernel)
+        o_ws, o_na, c_ws, c_na = both(q, cache, lens, kv_new, kernel, listed)
         assert np.array_equal(bits(o_na), bits(o_ws)), f"call {i}: outputs differ"
         assert np.array_equal(bits(c_na), bits(c_ws)), f"call {i}: appended caches differ"
         np.testing.assert_array_equal(bits(c_na), oracle.append(bits(cache), bits(kv_new), lens))

@@ -98,10 +98,10 @@ class Job:
         if ev is not None:
             ev[1].record()
         ops.unpack_live(self.packed, self.decode, w.lens)
-        self.positions.copy_(self.seqlens)
-        self.graph.restart()
         if ev is not None:
             ev[2].record()
+        self.positions.copy_(self.seqlens)
+        self.graph.restart()
         for t in range(w.decode_steps):
             self.graph.replay()
             if ev is not None:

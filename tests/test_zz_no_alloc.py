@@ -34,14 +34,16 @@ def stream_of(t):
 
 def both(q, cache, lens, kv_new, kernel, listed=False):
     """(workspace output, no-alloc output, cache after each) of one call;
-    ``listed``: both calls run the same host-planned work list (its device
-    buffers are the caller's inputs)."""
+    ``listed``: both calls run the same host-planned work list of
+    128-position items (its device buffers are the caller's inputs)."""
     lib = _lib.load()
     seqlens = torch.tensor(lens, dtype=torch.int32, device=q.device)
     max_seqlen = max(lens) + 1
     c_ws, c_na = cache.clone(), cache.clone()
     o_ws, o_na = torch.full_like(q, 7.0), torch.full_like(q, -7.0)
-    p = ops._attend_params(q, c_ws, o_ws, seqlens, 0, max_seqlen, kv_new, False, None, 0, kernel)
+    # The work list is cut into 128-position chunks so that both calls split.
+    p = ops._attend_params(q, c_ws, o_ws, seqlens, 0, max_seqlen, kv_new, False, None, 128 if listed else 0,
+                           kernel)
     work = ops._plan_work(p, lens, q.device) if listed else None
     if work:
         work.apply(p)

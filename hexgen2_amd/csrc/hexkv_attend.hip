@@ -1252,17 +1252,21 @@ namespace hexkv {
 // MI355X against the uniform grid and against each other (attention +
 // merge per layer, interleaved A/B in one process): below 4 MB the call is
 // launch-bound and no split at all is fastest (TinyLlama: 6.5 vs 8.1 us --
-// no merge launch); up to 64 MB it is latency-bound and about 200 items,
-// one per CU, are fastest (the Llama-2-70B TP-8 share: 384-position chunks
-// 13.3 us against 15.2 for the grid, 14.9 at 256, 14.7 at 512); above,
+// no merge launch).  Up to 64 MB a workgroup's stream, not HBM, is the
+// limit (about 22 GB/s per workgroup, one per CU, 4 or 8 waves alike), so
+// about 240 items, close to one per CU, are fastest: the Llama-2-70B TP-8
+// share (36 MB, read from HBM: twenty caches per measurement, more than the
+// 256 MB MALL) 13.4-13.7 us at 320 positions against 14.1 at 384, 14.2 at
+// 352, 14.8 at 448, 15.5 at 512 and 16.1 at 256.  Above 64 MB,
 // 1024-position chunks, or 1280 from a million positions up (Llama-2-7B,
-// 0.34 M positions: 31.4 us at 1024 against 33.6 for the grid and 34.6 at
-// 1280; Llama-3-8B, 2.0 M: 170.3-170.9 us at 1280 against 173.0-173.2 at
-// 1024, 179 for the grid and 179.6 at 512, over three boxes).
+// 0.34 M positions: 768, 1024 and equal pieces of 812 within 33.1-34.5 us
+// on HBM-resident data, 36.5 at 1280; Llama-3-8B, 2.0 M: 170.3-170.9 us at
+// 1280 against 173.0-173.2 at 1024, 179 for the grid and 179.6 at 512,
+// over three boxes).
 static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest) {
   const int64_t bytes = positions * row_bytes;
   if (bytes < (INT64_C(4) << 20)) return static_cast<int>(std::max<int64_t>(64, (longest + 63) / 64 * 64));
-  if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 200 + 63) / 64 * 64)));
+  if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 240 + 63) / 64 * 64)));
   return positions >= (INT64_C(1) << 20) ? 1280 : 1024;
 }
 

@@ -255,7 +255,7 @@ int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_w
 /*
  * The chunk (positions per work item) hexkv_attend_plan uses for these
  * lengths: p->partition when set, else the library's choice -- one chunk per
- * segment below 4 MB read, about 200 items below 64 MB, 1024 positions
+ * segment below 4 MB read, about 240 items below 64 MB, 1024 positions
  * above (1280 from 2^20 positions up).  A caller that replays one captured
  * launch over several steps plans every step with the chunk of its last
  * (longest) step, passed as p->partition, so the item and partition counts

@@ -158,7 +158,7 @@ def test_plan_chunk_regimes():
     # small call (< 4 MB read): one item per (row, head group), no merge
     arr, parts, mp = plan(params(1, 32, 4, 64, dtype=_lib.HEXKV_F16), [576])
     assert mp == 1 and len(arr) == 4
-    # latency-bound (< 64 MB): about 200 items
+    # latency-bound (< 64 MB): about 240 items
     lens = [538 + 37 * i for i in range(32)]
     arr, _, mp = plan(params(32, 8, 1, 128), lens)
     assert 150 <= len(arr) <= 300 and mp > 1
@@ -199,7 +199,7 @@ def plan_chunk(p, lens):
 
 @pytest.mark.parametrize("lens,hq,hkv,d,dtype", [
     ([576], 32, 4, 64, _lib.HEXKV_F16),                          # one chunk per segment
-    ([538 + 37 * i for i in range(32)], 8, 1, 128, _lib.HEXKV_BF16),  # about 200 items
+    ([538 + 37 * i for i in range(32)], 8, 1, 128, _lib.HEXKV_BF16),  # about 240 items
     ([2000 - 10 * i for i in range(64)], 32, 8, 128, _lib.HEXKV_BF16),
     ([8000 - 100 * i for i in range(64)], 32, 8, 128, _lib.HEXKV_BF16),
 ])

@@ -33,15 +33,62 @@ __device__ __forceinline__ f16x2 as_f16x2(unsigned int w) { return __builtin_bit
 
 // ---------------------------------------------------------------- device ---
 
-// Sum over aligned groups of `LPP` consecutive lanes; every lane of a group
-// ends with the group's total.  Groups of up to 16 lanes use DPP lane moves
-// (quad permutes, then half-row and row mirrors), wider groups ds_bpermute.
+// Cross-lane reductions, all VALU data movement (no LDS round trip):
+// partners within a 16-lane row move by DPP (quad permutes, half-row and row
+// mirrors, a row rotation of 8); the two rows of a pair and the two halves
+// of the wave are exchanged by gfx950's v_permlane16_swap /
+// v_permlane32_swap, which hand each lane its own value and its partner's
+// (lane layout pinned on the GPU: swap16(x, x) gives rows (0, 0, 2, 2) and
+// (1, 1, 3, 3), swap32(x, x) halves (0, 0) and (1, 1)).  In every step both
+// lanes of a pair combine the same two values, so every lane of a group ends
+// with bit-identical results.
 template <int CTRL>
 __device__ __forceinline__ float dpp_move(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
+// The value of lane l ^ OFF (OFF < 16) in lane l.
+template <int OFF>
+__device__ __forceinline__ float row_partner(float v) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8, "offset within a row");
+  if constexpr (OFF == 1) return dpp_move<0xB1>(v);  // quad_perm [1,0,3,2]
+  else if constexpr (OFF == 2) return dpp_move<0x4E>(v);  // quad_perm [2,3,0,1]
+  else if constexpr (OFF == 4) return dpp_move<0x1B>(dpp_move<0x141>(v));  // 7 - l in 8, then l ^ 3 in 4
+  else return dpp_move<0x128>(v);  // row_ror:8 = l ^ 8 in 16
+}
+
+// op(x, x of lane l ^ OFF) in lane l, for OFF a power of two below 64.
+template <int OFF, typename Op>
+__device__ __forceinline__ float xor_step(float v, Op op) {
+  if constexpr (OFF < 16) {
+    return op(v, row_partner<OFF>(v));
+  } else {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    unsigned a, b;
+    if constexpr (OFF == 16) {
+      const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      a = p[0];
+      b = p[1];
+    } else {
+      static_assert(OFF == 32, "offset");
+      const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      a = p[0];
+      b = p[1];
+    }
+    return op(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  }
+}
+
+struct AddOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Sum over aligned groups of `LPP` consecutive lanes; every lane of a group
+// ends with the group's total.
 template <int LPP>
 __device__ __forceinline__ float group_sum(float v) {
   static_assert(LPP >= 1 && LPP <= 64 && (LPP & (LPP - 1)) == 0, "LPP must be a power of two");
@@ -49,41 +96,30 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (LPP >= 4) v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
   if constexpr (LPP >= 8) v += dpp_move<0x141>(v);  // row_half_mirror: other quad of 8
   if constexpr (LPP >= 16) v += dpp_move<0x140>(v); // row_mirror: other half of 16
-  if constexpr (LPP >= 32) v += __shfl_xor(v, 16);
-  if constexpr (LPP >= 64) v += __shfl_xor(v, 32);
+  if constexpr (LPP >= 32) v = xor_step<16>(v, AddOp{});
+  if constexpr (LPP >= 64) v = xor_step<32>(v, AddOp{});
   return v;
 }
 
-// Butterfly step over lanes l and l ^ OFF (ds_bpermute).
-template <int OFF>
-__device__ __forceinline__ float xor_sum(float v) {
-  return v + __shfl_xor(v, OFF);
+// Total (sum or max) over every offset in [FROM, 64): over the lanes that
+// agree in their low log2(FROM) bits.
+template <int FROM, typename Op>
+__device__ __forceinline__ float reduce_from(float v, Op op) {
+  if constexpr (FROM < 64) return reduce_from<FROM * 2>(xor_step<FROM>(v, op), op);
+  else return v;
 }
 
-template <int OFF>
-__device__ __forceinline__ float xor_max(float v) {
-  return fmaxf(v, __shfl_xor(v, OFF));
-}
-
-// xor_sum / xor_max over every offset in [FROM, 64): the total over the
-// lanes that agree in their low log2(FROM) bits.
 template <int FROM>
 __device__ __forceinline__ float sum_from(float v) {
-  if constexpr (FROM < 64) return sum_from<FROM * 2>(xor_sum<FROM>(v));
-  else return v;
+  return reduce_from<FROM>(v, AddOp{});
 }
 
 template <int FROM>
 __device__ __forceinline__ float max_from(float v) {
-  if constexpr (FROM < 64) return max_from<FROM * 2>(xor_max<FROM>(v));
-  else return v;
+  return reduce_from<FROM>(v, MaxOp{});
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return max_from<1>(v); }
 
 // Element traits: 16-byte vector <-> fp32, dot products on packed pairs.
 template <typename T>

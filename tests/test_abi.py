@@ -190,3 +190,15 @@ def test_noalloc_scratch_limit_matches_header_and_rejects_oversized_calls(tmp_pa
     assert need > limit
     assert lib.hexkv_attend_noalloc(ctypes.byref(p), None) == _lib.HEXKV_EWORKSPACE
     assert b"static scratch" in lib.hexkv_last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """Without the built library every entry point raises (there is no CPU
+    path to fall back to): the loader names the missing file."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIBRARY", tmp_path / "libhexkv.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.load()
+    with pytest.raises(RuntimeError, match="missing"):
+        ops.attend_kernel(torch.zeros((1, 1, 8, 64), dtype=torch.float16),
+                          torch.zeros((1, 4, 2, 1, 64), dtype=torch.float16))

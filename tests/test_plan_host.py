@@ -234,3 +234,78 @@ def test_plan_takes_chunks_beyond_4096():
         assert rc == _lib.HEXKV_EINVAL
     rc, _ = plan_chunk(params(2, 8, 2, 64, max_seqlen=50), lens)
     assert rc == _lib.HEXKV_ERANGE
+
+
+def check_order(arr):
+    """Empty rows first, then every full chunk (all of one size), then the
+    shorter last chunks from the longest down."""
+    counts = arr[:, 5]
+    empty = arr[:, 6] == 0
+    n_empty = int(empty.sum())
+    assert empty[:n_empty].all(), "empty rows come first"
+    rest = counts[n_empty:]
+    if len(rest) == 0:
+        return
+    chunk = rest.max()
+    full = rest == chunk
+    # full chunks are the segments' non-final pieces plus any last piece of exactly one chunk
+    last_full = np.nonzero(full)[0].max() if full.any() else -1
+    tails = rest[last_full + 1:]
+    assert (np.diff(tails) <= 0).all(), "last chunks from the longest down"
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_plans(seed):
+    """Random geometries, lengths (empty rows included), biases, chunk
+    choices and append flags: every plan covers each attended position of
+    each (row, head group) exactly once, in the dispatch order, and
+    hexkv_attend_plan_chunk names the chunk it used."""
+    rng = np.random.default_rng(7000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 3, 4, 8, 16]))
+    hq, d = hkv * group, int(rng.choice([16, 32, 64, 128, 256]))
+    batch = int(rng.integers(1, 70))
+    lens = [int(x) for x in rng.integers(0, 10000, batch)]
+    if seed % 3 == 0:
+        lens[int(rng.integers(batch))] = 0
+    kv_new = bool(rng.integers(2))
+    bias = int(rng.integers(0, 5))
+    partition = int(rng.choice([0, 0, 64, 192, 1024, 4160, 8192]))
+    dtype = int(rng.choice([_lib.HEXKV_F16, _lib.HEXKV_BF16, _lib.HEXKV_F32]))
+    extra = 1 if kv_new else 0
+    p = params(batch, hq, hkv, d, dtype=dtype, bias=bias, max_seqlen=max(lens) + bias + extra,
+               kv_new=kv_new, partition=partition)
+    arr, parts, mp = plan(p, lens)
+    check_cover(arr, parts, lens, hq, hkv, bias=bias, extra=extra)
+    check_order(arr)
+    assert mp == max(1, int(arr[:, 3].max()))
+    rc, chunk = plan_chunk(p, lens)
+    assert rc == 0 and (partition == 0 or chunk == partition)
+    assert arr[:, 5].max() <= chunk
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_counts_only_grow_over_replays_at_a_fixed_chunk(seed):
+    """The property a captured decode graph relies on: with the chunk fixed
+    (the last replay's, as ReplayWorkLists chooses it), every replay's item
+    count and largest partition count are at most the next one's, so the
+    last replay's sizes bound the capture."""
+    rng = np.random.default_rng(8000 + seed)
+    hkv = int(rng.choice([1, 4, 8]))
+    hq = hkv * int(rng.choice([1, 4, 8]))
+    batch = int(rng.integers(1, 40))
+    lens = [int(x) for x in rng.integers(1, 6000, batch)]
+    replays = int(rng.integers(2, 80))
+    max_seqlen = max(lens) + replays  # replay k attends lens + k + 1 keys
+    last = params(batch, hq, hkv, 128, bias=replays - 1, max_seqlen=max_seqlen)
+    rc, chunk = plan_chunk(last, lens)
+    assert rc == 0
+    lib = _lib.load()
+    c_lens = (ctypes.c_int32 * batch)(*lens)
+    sizes = []
+    for k in range(replays):
+        p = params(batch, hq, hkv, 128, bias=k, max_seqlen=max_seqlen, partition=chunk)
+        n, mp = ctypes.c_int32(), ctypes.c_int32()
+        assert lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)) == 0
+        sizes.append((n.value, mp.value))
+    assert all(a[0] <= b[0] and a[1] <= b[1] for a, b in zip(sizes, sizes[1:]))

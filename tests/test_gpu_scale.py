@@ -20,6 +20,10 @@ cache -- is checked on the device through size-independent properties: the
 packed buffer is the live rows in batch order, the unpacked live rows equal
 the prefill cache's, and every row past a sequence's length still holds the
 sentinel (hexgen2/model.py:81, :101-108).
+
+The decode step as the bench runs it -- a captured graph replayed over
+host-planned work lists -- is compared bit for bit with eager work-list
+calls at each workload's real batch and lengths.
 """
 import numpy as np
 import pytest
@@ -116,4 +120,58 @@ def test_llama3_8b_full_handoff_round_trip(device):
     assert start == w.live_rows
     print("  round trip bit-exact, padding untouched", flush=True)
     del prefill, decode, packed, pi, di, ki
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name", ["tinyllama-1.1b", "llama2-7b", "llama2-70b-tp8", "llama3-8b"])
+def test_graph_work_lists_at_full_size(device, name):
+    """The decode step the bench times -- one HIP graph replay per step over
+    the host-planned work list, uploaded before each replay -- at the
+    workload's real batch and lengths (two layers, four replays): every
+    replay equals the eager work-list calls of the same step with the same
+    chunk, bit for bit (outputs and caches)."""
+    w = workload(name)
+    B, cap, layers, replays = w.batch, w.capacity, 2, 4
+    lens = list(w.lens)
+    max_seqlen = max(lens) + replays  # replay k attends lens + k + 1 keys
+    print(f"{name}: graph work lists, batch {B}, longest row {max_seqlen}", flush=True)
+    g = torch.Generator(device=device).manual_seed(w.seed + 300)
+    cache_e = torch.empty((layers, B, cap, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=device)
+    for l in range(layers):
+        cache_e[l].normal_(generator=g)
+    cache_g = cache_e.clone()
+    q = torch.empty((layers, B, 1, w.q_heads, w.head_dim), dtype=w.dtype, device=device)
+    kv_new = torch.empty((layers, B, 2, w.kv_heads, w.head_dim), dtype=w.dtype, device=device)
+    out_e = torch.empty((layers, B, 1, w.q_heads, w.head_dim), dtype=w.dtype, device=device)
+    out_g = torch.empty_like(out_e)
+    pos_e = torch.tensor(lens, dtype=torch.int32, device=device)
+    pos_g = pos_e.clone()
+    host = list(lens)
+    q.normal_(generator=g)
+    kv_new.normal_(generator=g)
+    # load the kernels eagerly once (on scratch copies) before capture
+    scratch = cache_e[0].clone()
+    ops.decode_attention(q[0], scratch, max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[0], lens=host)
+    del scratch
+    torch.cuda.synchronize()
+    graph = ops.DecodeStepGraph(q, cache_g, out_g, kv_new, pos_g, max_seqlen, lens=host)
+    lists = graph.lists
+    print(f"  chunk {lists.chunk}, captured items {lists.capacity}, partitions {lists.max_parts}", flush=True)
+    assert lists.replays == replays
+    for step in range(replays):
+        q.normal_(generator=g)
+        kv_new.normal_(generator=g)
+        for l in range(layers):
+            ops.decode_attention(q[l], cache_e[l], max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[l],
+                                 out=out_e[l], lens=host, partition=lists.chunk)
+        pos_e.add_(1)
+        host = [n + 1 for n in host]
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pos_g, pos_e), f"step {step}: positions differ"
+        assert torch.equal(out_g, out_e), f"step {step}: outputs differ"
+        assert torch.equal(cache_g, cache_e), f"step {step}: caches differ"
+        print(f"  replay {step}: bit-identical to the eager step", flush=True)
+    del cache_e, cache_g, graph
     torch.cuda.empty_cache()

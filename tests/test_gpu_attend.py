@@ -295,3 +295,28 @@ def test_attend_plan_work_list_matches_grid_over_steps(device, kernel):
             torch.testing.assert_close(o_list.float(), o_grid.float(), rtol=0, atol=8e-3)
             check(o_list, q[l], c_list[l], [n + t + 1 for n in lens], torch.bfloat16)
     assert torch.equal(c_list.view(torch.int16), c_grid.view(torch.int16))
+
+
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel", [(8, 1, 128, torch.bfloat16, "mfma"),
+                                                   (32, 8, 128, torch.bfloat16, "valu"),
+                                                   (32, 4, 64, torch.float16, "valu"),
+                                                   (4, 2, 256, torch.bfloat16, "valu")])
+def test_rows_with_hundreds_of_partitions(device, hq, hkv, d, dtype, kernel):
+    """A 20,000-position row cut into 64-position partitions has 313 of them:
+    the merge kernel stages their weights through LDS 256 at a time (the
+    path beyond its register fast path).  Grid and work list, with short
+    and empty rows beside it, against the float64 oracle."""
+    lens = [20000, 3, 0, 700]
+    cap = 20032
+    q, cache = make(len(lens), cap, hq, hkv, d, dtype, 9, device)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    print(f"attend {kernel} hq={hq} hkv={hkv} d={d} {dtype}: 313 partitions", flush=True)
+    live = [b for b, n in enumerate(lens) if n]
+    ref = oracle.attend(f64(q)[live], f64(cache)[live], [lens[b] for b in live])
+    for listed in (False, True):
+        out = ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=64, kernel=kernel,
+                                   lens=lens if listed else None)
+        torch.cuda.synchronize()
+        err = np.abs(f64(out)[live] - ref).max()
+        assert err <= TOL[dtype], f"{'work list' if listed else 'grid'}: max-abs {err}"
+        assert (out[2] == 0).all(), "empty row not zero"

@@ -30,24 +30,53 @@ def _require_device(*tensors: torch.Tensor) -> None:
                              f"no CPU fallback (got a tensor on {t.device})")
 
 
-def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+def _stream(t) -> ctypes.c_void_p:
+    """The current stream of the device ``t`` (a tensor or ``_Layer``) lives on."""
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _contiguous(shape, stride) -> bool:
+    """``Tensor.is_contiguous()`` of a view with these sizes and strides,
+    without building the view (size-1 dims are free; an empty view is
+    contiguous)."""
+    if 0 in shape:
+        return True
+    expected = 1
+    for n, st in zip(reversed(shape), reversed(stride)):
+        if n != 1 and st != expected:
+            return False
+        expected *= n
+    return True
+
+
+def _row_geometry_of(shape, stride, elem_size: int):
+    """(row_elems, row_bytes, seq_stride_rows) of a ``[B, S, *row]`` cache
+    given as sizes and strides."""
+    if len(shape) < 3:
+        raise ValueError(f"cache must be [batch, capacity, *row], got shape {tuple(shape)}")
+    row_elems = math.prod(shape[2:])
+    if shape[0] and shape[1] and not _contiguous(shape[2:], stride[2:]):
+        raise ValueError("cache rows (dims 2+) must be contiguous")
+    if shape[1] > 1 and stride[1] != row_elems:
+        raise ValueError("cache positions must be consecutive rows (stride(1) == row size)")
+    if shape[0] > 1 and stride[0] % row_elems:
+        raise ValueError("cache batch stride must be a whole number of rows")
+    seq_stride = stride[0] // row_elems if shape[0] > 1 else shape[1]
+    return row_elems, row_elems * elem_size, seq_stride
 
 
 def _row_geometry(cache: torch.Tensor):
     """(row_elems, row_bytes, seq_stride_rows) of a ``[B, S, *row]`` cache."""
-    if cache.dim() < 3:
-        raise ValueError(f"cache must be [batch, capacity, *row], got shape {tuple(cache.shape)}")
-    row_elems = math.prod(cache.shape[2:])
-    inner = cache[0, 0] if cache.shape[0] and cache.shape[1] else None
-    if inner is not None and not inner.is_contiguous():
-        raise ValueError("cache rows (dims 2+) must be contiguous")
-    if cache.shape[1] > 1 and cache.stride(1) != row_elems:
-        raise ValueError("cache positions must be consecutive rows (stride(1) == row size)")
-    if cache.shape[0] > 1 and cache.stride(0) % row_elems:
-        raise ValueError("cache batch stride must be a whole number of rows")
-    seq_stride = cache.stride(0) // row_elems if cache.shape[0] > 1 else cache.shape[1]
-    return row_elems, row_elems * cache.element_size(), seq_stride
+    return _row_geometry_of(tuple(cache.shape), cache.stride(), cache.element_size())
+
+
+class _Layer:
+    """Shape, dtype and device of one cache layer (``[B, S, *row]``)."""
+
+    __slots__ = ("shape", "dtype", "device")
+
+    def __init__(self, shape, dtype, device):
+        self.shape, self.dtype, self.device = shape, dtype, device
 
 
 def _as_layers(x: TensorList) -> list:
@@ -76,9 +105,10 @@ def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, 
             raise ValueError("packed and cache tensors differ in dtype or device")
         if packed.dim() < 1 or packed.shape[0] != n_layers:
             raise ValueError(f"packed tensor of shape {tuple(packed.shape)} for {n_layers} cache layers")
-        if packed[0].numel() != total * row_elems or not packed[0].is_contiguous():
+        shape, stride = tuple(packed.shape[1:]), packed.stride()[1:]
+        if math.prod(shape) != total * row_elems or not _contiguous(shape, stride):
             raise ValueError(f"packed layer must be contiguous with {total} rows of {row_elems} "
-                             f"elements, got shape {tuple(packed.shape[1:])}")
+                             f"elements, got shape {shape}")
         return _layer_ptrs(packed)
     layers = list(packed)
     if len(layers) != n_layers:
@@ -96,15 +126,17 @@ def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, 
 
 
 def _cache_ptrs(cache_layers: TensorList):
-    """(first layer, per-layer base addresses, row geometry) of the cache
-    layers: a list of ``[B, S, *row]`` tensors sharing shape, strides, dtype
-    and device, or one stacked ``[n_layers, B, S, *row]`` tensor."""
+    """(first layer's shape/dtype/device, per-layer base addresses, row
+    geometry) of the cache layers: a list of ``[B, S, *row]`` tensors sharing
+    shape, strides, dtype and device, or one stacked ``[n_layers, B, S,
+    *row]`` tensor (checked from its sizes and strides, no views built)."""
     if isinstance(cache_layers, torch.Tensor):
         if cache_layers.dim() < 1 or cache_layers.shape[0] == 0:
             raise ValueError("no cache layers")
         _require_device(cache_layers)
-        first = cache_layers[0]
-        return first, _layer_ptrs(cache_layers), _row_geometry(first)
+        shape = tuple(cache_layers.shape[1:])
+        geometry = _row_geometry_of(shape, cache_layers.stride()[1:], cache_layers.element_size())
+        return _Layer(shape, cache_layers.dtype, cache_layers.device), _layer_ptrs(cache_layers), geometry
     layers = list(cache_layers)
     if not layers:
         raise ValueError("no cache layers")
@@ -116,7 +148,7 @@ def _cache_ptrs(cache_layers: TensorList):
         if t.shape != first.shape or t.dtype != first.dtype or t.device != first.device \
                 or t.stride() != first.stride():
             raise ValueError("all cache layers must share shape, strides, dtype and device")
-    return first, [t.data_ptr() for t in layers], geometry
+    return _Layer(tuple(first.shape), first.dtype, first.device), [t.data_ptr() for t in layers], geometry
 
 
 def pack_live(cache_layers: TensorList, lens: Sequence[int],

@@ -4,13 +4,18 @@
 // the VALU kernel with a rotary prologue, K tiles staged through LDS to turn
 // the FT chunk planes back into position-major rows, V read directly).
 //
-// Work decomposition (split-K, "flash-decoding"):
-//   grid = (partition, q-head group, query row).  A workgroup (4 waves) owns
-//   `part` consecutive cache positions of one sequence for G query heads that
-//   share one KV head, so every K/V byte is read by exactly one workgroup.
-//   Ragged lengths only change how many partitions a row has; every
-//   partition but the last is full, so work per workgroup is uniform and
-//   small partitions keep the tail of the launch short.
+// Work decomposition (split-K, "flash-decoding"): a workgroup (4 waves) owns
+// consecutive cache positions of one sequence for the G query heads that
+// share one KV head, so every K/V byte is read by exactly one workgroup.  Two
+// ways to hand out those pieces:
+//   * grid = (partition, q-head group, query row), partitions of `part`
+//     positions, row lengths read from seqlens on the device; ragged lengths
+//     only change how many partitions a row has.
+//   * a work list (decode rows, lengths known on the host): workgroup i runs
+//     item i, planned by hexkv_attend_plan -- full chunks first, chunk index
+//     by chunk index across every (row, head group) segment, then each
+//     segment's shorter last chunk from the longest down -- so the grid has
+//     no empty partitions and the launch ends on its smallest items.
 //
 // Two kernels stream a partition; both keep every load in flight without a
 // barrier, address K/V as a uniform (SGPR) base plus a 32-bit lane offset,
@@ -43,7 +48,11 @@
 // and `combine_kernel`, launched next on the same stream, merges them.  (A
 // last-arriver merge inside the attention kernel needs an agent-scope release
 // per workgroup, which on this part writes back the whole L2 of the XCD and
-// serialises: measured 2-20x slower than the second launch.)
+// serialises: measured 2-20x slower than the second launch.  With
+// write-through partial stores and an arrival counter instead of the release
+// it still lost: the store wait, the counter round trip and the reload of
+// the partials sit on the last items' path, 178.8 against 176.1 us per
+// Llama-3-8B layer and 16.5 against 14.4 at the Llama-2-70B TP-8 share.)
 #include "hexkv_common.h"
 
 #include <algorithm>

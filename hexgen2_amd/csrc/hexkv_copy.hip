@@ -36,16 +36,28 @@ constexpr int kCopyUnroll = 8;
 // The per-step append moves one row per sequence: 512 threads, one vector each.
 constexpr int kAppendThreads = 512;
 
+// Kernel arguments of one launch over L layers and S sequences at most.  The
+// block is copied into the kernel-argument segment on every launch, and its
+// size shows in the host's cost per call: a hexkv_pack call of TinyLlama's
+// 22-layer handoff took 5.9 us with the 2.6 KB block of 96 layers x 256
+// sequences and 3.4-3.9 us with a 0.46 KB one (MI355X host, back-to-back
+// calls; the kernel itself takes 6.8 us, so the host set the rate of
+// isolated calls).  Launches of up to 32 layers and 16 sequences use the
+// 0.6 KB block.
+template <int L, int S>
 struct RaggedCopyArgs {
-  const char *src[HEXKV_MAX_LAYERS_PER_LAUNCH];
-  char *dst[HEXKV_MAX_LAYERS_PER_LAUNCH];
+  const char *src[L];
+  char *dst[L];
   int64_t row_bytes;
   int64_t seq_stride_bytes;  // padded (cache) side: bytes between sequences
   int64_t chunk_bytes;       // packed bytes per workgroup
   int64_t layer_bytes;       // packed bytes per layer in this launch
   int32_t batch;
-  int32_t cu[HEXKV_MAX_SEQS_PER_LAUNCH + 1];  // packed row offset of each sequence
+  int32_t cu[S + 1];  // packed row offset of each sequence
 };
+using WideCopyArgs = RaggedCopyArgs<HEXKV_MAX_LAYERS_PER_LAUNCH, HEXKV_MAX_SEQS_PER_LAUNCH>;
+using SmallCopyArgs = RaggedCopyArgs<32, 16>;
+static_assert(sizeof(WideCopyArgs) <= 4096, "kernel arguments above 4 KiB");
 
 // Every pass issues kCopyUnroll loads per lane before its stores; the last,
 // partial pass masks lanes instead of falling back to one vector at a time.
@@ -75,8 +87,8 @@ __device__ __forceinline__ void copy_span(const char *__restrict__ s, char *__re
 }
 
 // PACK: src = padded cache, dst = packed buffer.  UNPACK: the reverse.
-template <typename V, bool PACK>
-__global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const RaggedCopyArgs a) {
+template <typename V, bool PACK, typename A>
+__global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const A a) {
   const int64_t start = static_cast<int64_t>(blockIdx.x) * a.chunk_bytes;
   if (start >= a.layer_bytes) return;
   const int64_t end = min(start + a.chunk_bytes, a.layer_bytes);
@@ -126,6 +138,39 @@ static int64_t choose_chunk(int64_t total_bytes) {
   return std::min<int64_t>(std::max<int64_t>(chunk, 16384), 131072);
 }
 
+// One launch: layers [l0, l0 + nl) of sequences [b0, b0 + nb), whose packed
+// row offsets are cu[0..nb]; A is the argument block it fits.
+template <typename A>
+static int launch_copy(bool pack, bool vec16, const void *const *src_layers, void *const *dst_layers, int l0,
+                       int nl, int nb, const int32_t *cu, int64_t row_bytes, int64_t seq_stride_bytes,
+                       int64_t chunk, int64_t padded_off, int64_t packed_off, hipStream_t stream,
+                       const char *what) {
+  A a;
+  a.row_bytes = row_bytes;
+  a.seq_stride_bytes = seq_stride_bytes;
+  a.chunk_bytes = chunk;
+  a.batch = nb;
+  for (int b = 0; b <= nb; ++b) a.cu[b] = cu[b];
+  a.layer_bytes = static_cast<int64_t>(cu[nb]) * row_bytes;
+  for (int l = 0; l < nl; ++l) {
+    const char *s = static_cast<const char *>(src_layers[l0 + l]);
+    char *d = static_cast<char *>(dst_layers[l0 + l]);
+    a.src[l] = s + (pack ? padded_off : packed_off);
+    a.dst[l] = d + (pack ? packed_off : padded_off);
+  }
+  const int64_t gx = (a.layer_bytes + chunk - 1) / chunk;
+  if (gx > INT32_MAX) return fail(HEXKV_ERANGE, "%s: grid too large", what);
+  dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(nl));
+  if (vec16) {
+    if (pack) ragged_copy_kernel<u32x4, true, A><<<grid, kCopyThreads, 0, stream>>>(a);
+    else ragged_copy_kernel<u32x4, false, A><<<grid, kCopyThreads, 0, stream>>>(a);
+  } else {
+    if (pack) ragged_copy_kernel<unsigned int, true, A><<<grid, kCopyThreads, 0, stream>>>(a);
+    else ragged_copy_kernel<unsigned int, false, A><<<grid, kCopyThreads, 0, stream>>>(a);
+  }
+  return check_launch(what);
+}
+
 static int ragged_copy(bool pack, const void *const *src_layers, void *const *dst_layers,
                        int n_layers, int batch, int64_t seq_stride_rows, int64_t capacity,
                        int64_t row_bytes, const int64_t *lens, hipStream_t stream) {
@@ -161,39 +206,23 @@ static int ragged_copy(bool pack, const void *const *src_layers, void *const *ds
   // Sequences in groups of HEXKV_MAX_SEQS_PER_LAUNCH, layers in groups of
   // HEXKV_MAX_LAYERS_PER_LAUNCH; one launch per (group, group) pair.
   int64_t row_base = 0;
+  int32_t cu[HEXKV_MAX_SEQS_PER_LAUNCH + 1];
+  const int64_t seq_stride_bytes = seq_stride_rows * row_bytes;
   for (int b0 = 0; b0 < batch; b0 += HEXKV_MAX_SEQS_PER_LAUNCH) {
     const int nb = std::min(batch - b0, HEXKV_MAX_SEQS_PER_LAUNCH);
-    RaggedCopyArgs a;
-    a.row_bytes = row_bytes;
-    a.seq_stride_bytes = seq_stride_rows * row_bytes;
-    a.chunk_bytes = chunk;
-    a.batch = nb;
-    a.cu[0] = 0;
-    for (int b = 0; b < nb; ++b) a.cu[b + 1] = a.cu[b] + static_cast<int32_t>(lens[b0 + b]);
-    a.layer_bytes = static_cast<int64_t>(a.cu[nb]) * row_bytes;
-    const int64_t padded_off = static_cast<int64_t>(b0) * seq_stride_rows * row_bytes;
+    cu[0] = 0;
+    for (int b = 0; b < nb; ++b) cu[b + 1] = cu[b] + static_cast<int32_t>(lens[b0 + b]);
+    const int64_t padded_off = static_cast<int64_t>(b0) * seq_stride_bytes;
     const int64_t packed_off = row_base * row_bytes;
-    row_base += a.cu[nb];
-    if (a.layer_bytes == 0) continue;
-    const int64_t gx = (a.layer_bytes + chunk - 1) / chunk;
-    if (gx > INT32_MAX) return fail(HEXKV_ERANGE, "%s: grid too large", what);
+    row_base += cu[nb];
+    if (cu[nb] == 0) continue;
     for (int l0 = 0; l0 < n_layers; l0 += HEXKV_MAX_LAYERS_PER_LAUNCH) {
       const int nl = std::min(n_layers - l0, HEXKV_MAX_LAYERS_PER_LAUNCH);
-      for (int l = 0; l < nl; ++l) {
-        const char *s = static_cast<const char *>(src_layers[l0 + l]);
-        char *d = static_cast<char *>(dst_layers[l0 + l]);
-        a.src[l] = s + (pack ? padded_off : packed_off);
-        a.dst[l] = d + (pack ? packed_off : padded_off);
-      }
-      dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(nl));
-      if (vec16) {
-        if (pack) ragged_copy_kernel<u32x4, true><<<grid, kCopyThreads, 0, stream>>>(a);
-        else ragged_copy_kernel<u32x4, false><<<grid, kCopyThreads, 0, stream>>>(a);
-      } else {
-        if (pack) ragged_copy_kernel<unsigned int, true><<<grid, kCopyThreads, 0, stream>>>(a);
-        else ragged_copy_kernel<unsigned int, false><<<grid, kCopyThreads, 0, stream>>>(a);
-      }
-      int rc = check_launch(what);
+      const int rc = nl <= 32 && nb <= 16
+          ? launch_copy<SmallCopyArgs>(pack, vec16, src_layers, dst_layers, l0, nl, nb, cu, row_bytes,
+                                       seq_stride_bytes, chunk, padded_off, packed_off, stream, what)
+          : launch_copy<WideCopyArgs>(pack, vec16, src_layers, dst_layers, l0, nl, nb, cu, row_bytes,
+                                      seq_stride_bytes, chunk, padded_off, packed_off, stream, what);
       if (rc != HEXKV_OK) return rc;
     }
   }

@@ -10,7 +10,9 @@ validated on the host before anything is launched.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
+from collections import OrderedDict
 from typing import Optional, Sequence, Union
 
 import torch
@@ -30,8 +32,16 @@ def _require_device(*tensors: torch.Tensor) -> None:
                              f"no CPU fallback (got a tensor on {t.device})")
 
 
+# torch's own accessor of the current stream's handle (what
+# ``torch.cuda.current_stream(device).cuda_stream`` returns, without building
+# a Stream object: 0.1 us against 1.9 us a call on MI355X's host).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t) -> ctypes.c_void_p:
     """The current stream of the device ``t`` (a tensor or ``_Layer``) lives on."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
@@ -49,6 +59,7 @@ def _contiguous(shape, stride) -> bool:
     return True
 
 
+@functools.lru_cache(maxsize=256)
 def _row_geometry_of(shape, stride, elem_size: int):
     """(row_elems, row_bytes, seq_stride_rows) of a ``[B, S, *row]`` cache
     given as sizes and strides."""
@@ -90,11 +101,27 @@ def _check_lens(lens: Sequence[int], batch: int) -> list:
     return lens
 
 
-def _layer_ptrs(stacked: torch.Tensor) -> list:
-    """Base address of each layer of a stacked ``[n_layers, ...]`` tensor."""
-    step = stacked.stride(0) * stacked.element_size()
-    base = stacked.data_ptr()
-    return [base + l * step for l in range(stacked.shape[0])]
+_LAYER_ARRAYS: "OrderedDict[tuple, ctypes.Array]" = OrderedDict()
+
+
+def _layer_ptrs(stacked: torch.Tensor) -> ctypes.Array:
+    """Base address of each layer of a stacked ``[n_layers, ...]`` tensor, as
+    the ``void *[]`` the C entry points take.  The array depends only on
+    (address, layer stride, layer count), so recently used ones are kept and
+    handed out again (the C side only reads them)."""
+    key = (stacked.data_ptr(), stacked.stride(0) * stacked.element_size(), stacked.shape[0])
+    arr = _LAYER_ARRAYS.get(key)
+    if arr is None:
+        base, step, n = key
+        arr = (ctypes.c_void_p * n)(*[base + l * step for l in range(n)])
+        _LAYER_ARRAYS[key] = arr
+        if len(_LAYER_ARRAYS) > 64:
+            _LAYER_ARRAYS.popitem(last=False)
+    return arr
+
+
+def _ptr_array(ptrs: list) -> ctypes.Array:
+    return (ctypes.c_void_p * len(ptrs))(*ptrs)
 
 
 def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, dtype, device):
@@ -122,7 +149,7 @@ def _packed_ptrs(packed: TensorList, n_layers: int, total: int, row_elems: int, 
             raise ValueError(f"packed layer must be contiguous with {total} rows of {row_elems} "
                              f"elements, got shape {tuple(t.shape)}")
         ptrs.append(t.data_ptr())
-    return ptrs
+    return _ptr_array(ptrs)
 
 
 def _cache_ptrs(cache_layers: TensorList):
@@ -148,7 +175,7 @@ def _cache_ptrs(cache_layers: TensorList):
         if t.shape != first.shape or t.dtype != first.dtype or t.device != first.device \
                 or t.stride() != first.stride():
             raise ValueError("all cache layers must share shape, strides, dtype and device")
-    return _Layer(tuple(first.shape), first.dtype, first.device), [t.data_ptr() for t in layers], geometry
+    return _Layer(tuple(first.shape), first.dtype, first.device), _ptr_array([t.data_ptr() for t in layers]), geometry
 
 
 def pack_live(cache_layers: TensorList, lens: Sequence[int],
@@ -169,9 +196,7 @@ def pack_live(cache_layers: TensorList, lens: Sequence[int],
         out = torch.empty((len(layers), total, *first.shape[2:]), dtype=first.dtype,
                           device=first.device)
     dst = _packed_ptrs(out, len(layers), total, row_elems, first.dtype, first.device)
-    n = len(layers)
-    rc = _lib.load().hexkv_pack((ctypes.c_void_p * n)(*layers),
-                                (ctypes.c_void_p * n)(*dst), n, len(lens), seq_stride,
+    rc = _lib.load().hexkv_pack(layers, dst, len(layers), len(lens), seq_stride,
                                 first.shape[1], row_bytes, (ctypes.c_int64 * len(lens))(*lens),
                                 _stream(first))
     _lib.check(rc, "hexkv_pack")
@@ -185,9 +210,7 @@ def unpack_live(packed: TensorList, cache_layers: TensorList, lens: Sequence[int
     first, layers, (row_elems, row_bytes, seq_stride) = _cache_ptrs(cache_layers)
     lens = _check_lens(lens, first.shape[0])
     src = _packed_ptrs(packed, len(layers), sum(lens), row_elems, first.dtype, first.device)
-    n = len(layers)
-    rc = _lib.load().hexkv_unpack((ctypes.c_void_p * n)(*src),
-                                  (ctypes.c_void_p * n)(*layers), n,
+    rc = _lib.load().hexkv_unpack(src, layers, len(layers),
                                   len(lens), seq_stride, first.shape[1], row_bytes,
                                   (ctypes.c_int64 * len(lens))(*lens), _stream(first))
     _lib.check(rc, "hexkv_unpack")

@@ -72,6 +72,35 @@ def test_pack_many_layers_and_sequences_split_launches(device):
         np.testing.assert_array_equal(bits(dst[l]), want[l])
 
 
+@pytest.mark.parametrize("n_layers,batch", [(32, 16), (33, 16), (32, 17), (100, 10)])
+def test_launches_around_the_small_argument_block(device, n_layers, batch):
+    # launches of up to 32 layers and 16 sequences carry a small kernel-argument
+    # block, larger ones the full one; 100 layers = a full launch of 96, then 4
+    print(f"argument block layers={n_layers} batch={batch}", flush=True)
+    lens = [int(x) for x in np.random.default_rng(n_layers + batch).integers(0, 9, size=batch)]
+    layers = rand_layers(n_layers, batch, 9, (2, 1, 8), torch.float16, 4, device)
+    packed = ops.pack_live(layers, lens)
+    expect = oracle.pack([bits(t) for t in layers], lens)
+    np.testing.assert_array_equal(bits(packed), expect)
+    dst = [torch.full_like(layers[0], 5.0) for _ in range(n_layers)]
+    ops.unpack_live(packed, dst, lens)
+    want = oracle.unpack(expect, [bits(dst[0])] * n_layers, lens)
+    for l in range(n_layers):
+        np.testing.assert_array_equal(bits(dst[l]), want[l])
+
+
+def test_launches_follow_the_current_stream(device):
+    layers = rand_layers(3, 2, 6, (2, 1, 8), torch.float16, 8, device)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert (ops._stream(layers[0]).value or 0) == side.cuda_stream
+        packed = ops.pack_live(layers, [6, 2])
+    # the default stream's handle is 0, which ctypes reads back as None
+    assert (ops._stream(layers[0]).value or 0) == torch.cuda.current_stream().cuda_stream
+    side.synchronize()
+    np.testing.assert_array_equal(bits(packed), oracle.pack([bits(t) for t in layers], [6, 2]))
+
+
 def test_pack_into_per_layer_views_and_strided_batch(device):
     # caches that are batch slices of a larger allocation (batch_size_offset)
     big = rand_layers(2, 5, 10, (2, 2, 16), torch.bfloat16, 5, device)

@@ -108,7 +108,7 @@ class Engine:
                            device=self.device, dtype=self.dtype)
         live = [cache[i].to(self.device) for i in range(n_layers)]
         live = [t if t.is_contiguous() else t.contiguous() for t in live]
-        ops.unpack_live(live, list(full.unbind(0)), [prompt_length])
+        ops.unpack_live(live, full, [prompt_length])
         for i in range(n_layers):
             state.key_value_memory_dict[i] = full[i]
         for _ in range(max_new_tokens - 1):

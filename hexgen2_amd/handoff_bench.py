@@ -3,9 +3,12 @@
 The two-rank pilot (hexgen2/run.py:141-198) hands each request's KV packet
 from the prefill rank to the decode rank; the reference moves it through
 host memory and TCP (hexgen2/transport.py:44-100).  Here rank 0 packs the
-prefill cache into one packet tensor per layer (each its own allocation,
-below the 2 GiB IPC limit) and sends it through ``IpcChannel``: the header
-goes over a Gloo group, the bytes stay where rank 0's pack kernel wrote them.
+prefill cache into one packet tensor per layer and sends it through
+``IpcChannel``: the header goes over a Gloo group, the bytes stay where rank
+0's pack kernel wrote them.  As in ``Engine.prefill``, a packet below 1 GiB
+is one packed allocation whose layers are views (one handle export, one
+mapping), a larger one one allocation per layer (each below the 2 GiB IPC
+limit).
 Rank 1 maps them and unpacks straight from rank 0's memory into its decode
 cache.  Per round, one JSON line per rank:
 
@@ -38,6 +41,7 @@ import torch.multiprocessing as mp
 
 def _worker(rank: int, rendezvous: str, workload_name: str, rounds: int) -> None:
     from . import ops
+    from .engine import PER_LAYER_HANDOFF_BYTES
     from .transport import IpcChannel, recv_packet, send_packet
     from .workloads import workload
 
@@ -55,7 +59,10 @@ def _worker(rank: int, rendezvous: str, workload_name: str, rounds: int) -> None
         if rank == 0:
             g = torch.Generator(device="cuda").manual_seed(w.seed + 1)
             prefill = [torch.empty(shape, dtype=w.dtype, device="cuda").normal_(generator=g) for _ in range(L)]
-            packed = [torch.empty((rows, *shape[2:]), dtype=w.dtype, device="cuda") for _ in range(L)]
+            if L * rows * w.row_bytes < PER_LAYER_HANDOFF_BYTES:
+                packed = list(torch.empty((L, rows, *shape[2:]), dtype=w.dtype, device="cuda").unbind(0))
+            else:
+                packed = [torch.empty((rows, *shape[2:]), dtype=w.dtype, device="cuda") for _ in range(L)]
             ops.pack_live(prefill, w.lens, out=packed)
             torch.cuda.synchronize()
             del prefill
@@ -68,7 +75,8 @@ def _worker(rank: int, rendezvous: str, workload_name: str, rounds: int) -> None
                 reply, _ = recv_packet(src=1, channel=channel)  # rank 1 is done with the packet
                 del reply
                 print(json.dumps({"rank": 0, "workload": w.name, "round": rnd, "send_ms": round((t1 - t0) / 1e6, 3),
-                                  "layers": L, "packet_bytes": L * rows * w.row_bytes}), flush=True)
+                                  "layers": L, "packet_bytes": L * rows * w.row_bytes,
+                                  "allocations": len({t.untyped_storage().data_ptr() for t in packed})}), flush=True)
         else:
             decode = [torch.empty(shape, dtype=w.dtype, device="cuda") for _ in range(L)]
             local = None

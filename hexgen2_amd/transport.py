@@ -160,9 +160,12 @@ class IpcChannel:
     the bytes are complete, and sends over ``torch.distributed`` (``group``;
     host tensors only): the int64 header length, the header, then one
     80-byte descriptor per tensor (IPC handle of the allocation holding it,
-    byte offset, allocation size).  ``recv`` maps the allocations and returns
-    tensors that alias the sender's memory (zero-size tensors are created
-    locally).
+    byte offset, allocation size).  ``recv`` maps each allocation once and
+    returns tensors that alias the sender's memory, views of one byte tensor
+    over the mapping (zero-size tensors are created locally).  Tensors of one
+    packet that share an allocation (the layers of one packed buffer) cost
+    one handle export and one mapping, not one each: an export takes ~9 us
+    of host time on MI355X.
 
     Lifetime protocol: the sender keeps every tensor of a packet alive until
     it next receives a packet from that peer; the receiver must drop the
@@ -181,6 +184,7 @@ class IpcChannel:
         encoded, payload = _encode_header(tensors, metadata, self.max_payload)
         lib = _lib.load()
         items, descriptors = [], bytearray()
+        exported = {}  # storage address -> (handle, storage's offset in its allocation, allocation bytes)
         for name, tensor in tensors.items():
             tensor = tensor.detach()
             if not tensor.is_cuda:
@@ -190,13 +194,18 @@ class IpcChannel:
             if tensor.numel() == 0:
                 descriptors += _DESCRIPTOR.pack(bytes(64), 0, 0)
                 continue
-            handle, offset, size = _lib.IpcHandle(), ctypes.c_uint64(), ctypes.c_uint64()
-            _lib.check(lib.hexkv_ipc_export(tensor.data_ptr(), ctypes.byref(handle), ctypes.byref(offset),
-                                            ctypes.byref(size)), "hexkv_ipc_export")
-            if size.value >= IPC_ALLOCATION_LIMIT:
-                raise ValueError(f"tensor {name!r} lives in a {size.value}-byte allocation; IPC handoff "
-                                 "needs allocations below 2 GiB (send it in per-layer tensors)")
-            descriptors += _DESCRIPTOR.pack(bytes(handle.bytes), offset.value, size.value)
+            storage = tensor.untyped_storage().data_ptr()
+            entry = exported.get(storage)
+            if entry is None:
+                handle, offset, size = _lib.IpcHandle(), ctypes.c_uint64(), ctypes.c_uint64()
+                _lib.check(lib.hexkv_ipc_export(storage, ctypes.byref(handle), ctypes.byref(offset),
+                                                ctypes.byref(size)), "hexkv_ipc_export")
+                if size.value >= IPC_ALLOCATION_LIMIT:
+                    raise ValueError(f"tensor {name!r} lives in a {size.value}-byte allocation; IPC handoff "
+                                     "needs allocations below 2 GiB (send it in per-layer tensors)")
+                entry = exported[storage] = (bytes(handle.bytes), offset.value, size.value)
+            handle_bytes, storage_offset, alloc = entry
+            descriptors += _DESCRIPTOR.pack(handle_bytes, storage_offset + (tensor.data_ptr() - storage), alloc)
         torch.cuda.current_stream().synchronize()
         dist.send(torch.tensor([len(encoded)], dtype=torch.int64), dst=dst, group=self.group)
         dist.send(torch.frombuffer(bytearray(encoded), dtype=torch.uint8), dst=dst, group=self.group)
@@ -220,28 +229,32 @@ class IpcChannel:
         raw = descriptors.numpy().tobytes()
         lib = _lib.load()
         device = torch.cuda.current_device()
-        tensors = {}
+        tensors, mapped = {}, {}  # mapped: handle -> (uint8 tensor over the whole allocation)
         for i, item in enumerate(header["tensors"]):
             handle_bytes, offset, alloc = _DESCRIPTOR.unpack_from(raw, i * _DESCRIPTOR.size)
             dtype, shape = DTYPES[item["dtype"]], item["shape"]
-            nbytes = math.prod(shape) * _ELEMENT_BYTES[item["dtype"]]
+            elem = _ELEMENT_BYTES[item["dtype"]]
+            nbytes = math.prod(shape) * elem
             if nbytes == 0:
                 tensors[item["name"]] = torch.empty(shape, dtype=dtype, device=device)
                 continue
-            if offset + nbytes > alloc:
+            if offset + nbytes > alloc or offset % elem:
                 raise ValueError("IPC descriptor does not cover the tensor its header names")
-            handle = _lib.IpcHandle()
-            ctypes.memmove(handle.bytes, handle_bytes, 64)
-            base = ctypes.c_void_p()
-            _lib.check(lib.hexkv_ipc_open(ctypes.byref(handle), ctypes.byref(base)), "hexkv_ipc_open")
-            code, bits = _DLPACK[dtype]
-            dims = (ctypes.c_int64 * max(1, len(shape)))(*shape)
-            managed = lib.hexkv_ipc_dlpack(base, offset, len(shape), dims, code, bits, device)
-            if not managed:
-                lib.hexkv_ipc_close(base)
-                raise ValueError(lib.hexkv_last_error().decode())
-            tensors[item["name"]] = torch.utils.dlpack.from_dlpack(
-                _capsule_new(managed, _CAPSULE_NAME, None))
+            whole = mapped.get((handle_bytes, alloc))
+            if whole is None:
+                handle = _lib.IpcHandle()
+                ctypes.memmove(handle.bytes, handle_bytes, 64)
+                base = ctypes.c_void_p()
+                _lib.check(lib.hexkv_ipc_open(ctypes.byref(handle), ctypes.byref(base)), "hexkv_ipc_open")
+                code, bits = _DLPACK[torch.uint8]
+                managed = lib.hexkv_ipc_dlpack(base, 0, 1, (ctypes.c_int64 * 1)(alloc), code, bits, device)
+                if not managed:
+                    lib.hexkv_ipc_close(base)
+                    raise ValueError(lib.hexkv_last_error().decode())
+                # the mapping is released when this tensor and every view of it are gone
+                whole = mapped[(handle_bytes, alloc)] = torch.utils.dlpack.from_dlpack(
+                    _capsule_new(managed, _CAPSULE_NAME, None))
+            tensors[item["name"]] = whole[offset:offset + nbytes].view(dtype).view(shape)
         return tensors, header["metadata"]
 
 

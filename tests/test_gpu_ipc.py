@@ -30,10 +30,16 @@ def _worker(rank, rendezvous):
                      2: torch.full((1, 3, 2, 1, 4), -1.25, dtype=dtype, device="cuda")}
             token = torch.tensor([42, 17], dtype=torch.long, device="cuda")
             big = torch.randn((3, 1000, 2, 8, 128), generator=g, device="cuda").to(dtype)
+            # tensors sharing one allocation: one export, one mapping, several views
+            stacked = torch.randn((4, 33, 2, 8), generator=g, device="cuda").to(dtype)
+            raw = torch.arange(64, dtype=torch.uint8, device="cuda")
+            shared = {f"l{i}": stacked[i] for i in range(4)}
+            shared.update(mid=stacked[1, 5:9], words=raw[8:40].view(torch.int64), byte=raw[3:4])
             if rank == 0:
                 send_data(token, cache, dst=1, channel=channel)
                 send_packet({"big": big, "empty": torch.zeros((0, 5), device="cuda")}, {"round": round_}, dst=1,
                             channel=channel)
+                send_packet(shared, {"shared": round_}, dst=1, channel=channel)
                 # the peer checks the bytes against this copy sent by value
                 dist.send(big.cpu(), dst=1)
                 received, returned = recv_data(src=1, num_layers=2, channel=channel)
@@ -44,6 +50,13 @@ def _worker(rank, rendezvous):
             else:
                 received, returned = recv_data(src=0, num_layers=2, channel=channel)
                 tensors, meta = recv_packet(src=0, channel=channel)
+                views, view_meta = recv_packet(src=0, channel=channel)
+                assert view_meta == {"shared": round_} and list(views) == list(shared)
+                for name, want in shared.items():
+                    got = views[name]
+                    assert got.is_cuda and got.dtype == want.dtype and got.shape == want.shape, name
+                    assert torch.equal(got.cpu(), want.cpu()), name
+                del views
                 expect = torch.empty((3, 1000, 2, 8, 128), dtype=dtype)
                 dist.recv(expect, src=0)
                 assert meta == {"round": round_}

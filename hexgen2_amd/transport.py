@@ -158,9 +158,10 @@ class IpcChannel:
     ``send`` encodes and validates the header exactly as the wire does, makes
     every tensor contiguous on the device, synchronises the sender's stream so
     the bytes are complete, and sends over ``torch.distributed`` (``group``;
-    host tensors only): the int64 header length, the header, then one
-    80-byte descriptor per tensor (IPC handle of the allocation holding it,
-    byte offset, allocation size).  ``recv`` maps each allocation once and
+    host tensors only): the header's and the descriptors' lengths (int64),
+    then one message of the header followed by one 80-byte descriptor per
+    tensor (IPC handle of the allocation holding it, byte offset, allocation
+    size).  ``recv`` maps each allocation once and
     returns tensors that alias the sender's memory, views of one byte tensor
     over the mapping (zero-size tensors are created locally).  Tensors of one
     packet that share an allocation (the layers of one packed buffer) cost
@@ -207,26 +208,28 @@ class IpcChannel:
             handle_bytes, storage_offset, alloc = entry
             descriptors += _DESCRIPTOR.pack(handle_bytes, storage_offset + (tensor.data_ptr() - storage), alloc)
         torch.cuda.current_stream().synchronize()
-        dist.send(torch.tensor([len(encoded)], dtype=torch.int64), dst=dst, group=self.group)
-        dist.send(torch.frombuffer(bytearray(encoded), dtype=torch.uint8), dst=dst, group=self.group)
-        dist.send(torch.frombuffer(descriptors, dtype=torch.uint8), dst=dst, group=self.group)
+        dist.send(torch.tensor([len(encoded), len(descriptors)], dtype=torch.int64), dst=dst, group=self.group)
+        dist.send(torch.frombuffer(bytearray(encoded) + descriptors, dtype=torch.uint8), dst=dst, group=self.group)
         self._held[dst].append(items)
         return payload
 
     def recv(self, src: int):
         from . import _lib
         self._held[src].clear()  # the peer has dropped our earlier packets
-        length = torch.empty(1, dtype=torch.int64)
-        dist.recv(length, src=src, group=self.group)
-        size = int(length.item())
+        lengths = torch.empty(2, dtype=torch.int64)
+        dist.recv(lengths, src=src, group=self.group)
+        size, described = (int(n) for n in lengths.tolist())
         if not 0 < size <= MAX_HEADER:
             raise ValueError("Invalid tensor header length")
-        encoded = torch.empty(size, dtype=torch.uint8)
-        dist.recv(encoded, src=src, group=self.group)
-        header = _decode_header(bytes(encoded.numpy().tobytes()), self.max_payload)
-        descriptors = torch.empty(_DESCRIPTOR.size * len(header["tensors"]), dtype=torch.uint8)
-        dist.recv(descriptors, src=src, group=self.group)
-        raw = descriptors.numpy().tobytes()
+        if not 0 <= described <= _DESCRIPTOR.size * MAX_TENSORS:
+            raise ValueError("Invalid IPC descriptor length")
+        message = torch.empty(size + described, dtype=torch.uint8)
+        dist.recv(message, src=src, group=self.group)
+        data = message.numpy().tobytes()
+        header = _decode_header(data[:size], self.max_payload)
+        if described != _DESCRIPTOR.size * len(header["tensors"]):
+            raise ValueError("IPC descriptors do not match the header's tensors")
+        raw = data[size:]
         lib = _lib.load()
         device = torch.cuda.current_device()
         tensors, mapped = {}, {}  # mapped: handle -> (uint8 tensor over the whole allocation)

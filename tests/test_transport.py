@@ -148,3 +148,46 @@ def test_device_channel_keeps_wire_validation_on_cpu_tensors():
     limited, peer = DeviceChannel.pair(max_payload=100)
     with pytest.raises(ValueError):
         send_packet({"x": torch.zeros(101, dtype=torch.uint8)}, {}, dst=1, channel=limited)
+
+
+def _ipc_control_peer(rank, rendezvous, failures):
+    """Rank 0 hand-crafts IpcChannel control messages; rank 1's recv must
+    reject each before it maps anything (no GPU is touched)."""
+    from hexgen2_amd.transport import IpcChannel
+    torch.set_num_threads(1)
+    dist.init_process_group("gloo", rank=rank, world_size=2, init_method=Path(rendezvous).as_uri(),
+                            timeout=timedelta(seconds=30))
+    header, _ = _encode_header({"x": torch.zeros(2)}, {}, 1 << 62)
+    cases = [(len(header), 2 * 80, "do not match"),  # two descriptors for one tensor
+             (len(header), 80 * 1025, "descriptor length"),
+             (0, 80, "header length")]
+    try:
+        for size, described, _ in cases:
+            if rank == 0:
+                dist.send(torch.tensor([size, described], dtype=torch.int64), dst=1)
+                if described == 2 * 80:
+                    dist.send(torch.frombuffer(bytearray(header) + bytes(described), dtype=torch.uint8), dst=1)
+            else:
+                with pytest.raises(ValueError) as caught:
+                    IpcChannel().recv(src=0)
+                assert [m for s, d, m in cases if (s, d) == (size, described)][0] in str(caught.value)
+    except Exception as error:
+        failures.put((rank, repr(error)))
+        raise
+    finally:
+        dist.destroy_process_group()
+
+
+def test_ipc_channel_rejects_bad_control_messages(tmp_path):
+    ctx = mp.get_context("spawn")
+    failures = ctx.SimpleQueue()
+    procs = [ctx.Process(target=_ipc_control_peer, args=(r, str(tmp_path / "rendezvous"), failures)) for r in (0, 1)]
+    for p in procs:
+        p.start()
+    for p in procs:
+        p.join(120)
+    seen = []
+    while not failures.empty():
+        seen.append(failures.get())
+    assert not seen, seen
+    assert [p.exitcode for p in procs] == [0, 0]

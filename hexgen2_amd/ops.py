@@ -256,21 +256,25 @@ def _attend_params(q, cache, out, seqlens, seqlen_bias, max_seqlen, kv_new, caus
     kv_heads = cache.shape[3]
     if q_heads % kv_heads:
         raise ValueError("q_heads must be a multiple of kv_heads")
-    for name, t in (("q", q), ("out", out)):
-        if t.stride(3) != 1 or t.stride(2) != head_dim:
-            raise ValueError(f"{name} heads must be contiguous [.., heads, head_dim]")
-    if cache.stride(4) != 1 or cache.stride(3) != head_dim:
+    if out.shape != q.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} differs from q shape {tuple(q.shape)}")
+    qs, os_, cs = q.stride(), out.stride(), cache.stride()
+    if qs[3] != 1 or qs[2] != head_dim:
+        raise ValueError("q heads must be contiguous [.., heads, head_dim]")
+    if os_[3] != 1 or os_[2] != head_dim:
+        raise ValueError("out heads must be contiguous [.., heads, head_dim]")
+    if cs[4] != 1 or cs[3] != head_dim:
         raise ValueError("cache heads must be contiguous [.., kv_heads, head_dim]")
     p = _lib.AttendParams()
     p.dtype = _DTYPES[q.dtype]
     p.batch, p.q_len, p.q_heads, p.kv_heads, p.head_dim = batch, q_len, q_heads, kv_heads, head_dim
     p.causal = 1 if causal else 0
     p.softmax_scale = float(head_dim ** -0.5 if softmax_scale is None else softmax_scale)
-    p.q, p.q_batch_stride, p.q_row_stride = q.data_ptr(), q.stride(0), q.stride(1)
+    p.q, p.q_batch_stride, p.q_row_stride = q.data_ptr(), qs[0], qs[1]
     p.cache = cache.data_ptr()
-    p.cache_batch_stride, p.cache_pos_stride, p.cache_kv_stride = cache.stride(0), cache.stride(1), cache.stride(2)
+    p.cache_batch_stride, p.cache_pos_stride, p.cache_kv_stride = cs[0], cs[1], cs[2]
     p.capacity = cache.shape[1]
-    p.out, p.out_batch_stride, p.out_row_stride = out.data_ptr(), out.stride(0), out.stride(1)
+    p.out, p.out_batch_stride, p.out_row_stride = out.data_ptr(), os_[0], os_[1]
     if seqlens is not None:
         _require_device(seqlens)
         if seqlens.dtype != torch.int32 or seqlens.numel() < batch or not seqlens.is_contiguous():
@@ -460,6 +464,8 @@ def _ft_params(q, k_new, v_new, k_cache, v_cache, out, positions, position_bias,
             raise ValueError(f"{name} {tuple(t.shape)} must be [batch, kv_heads, head_dim]")
     if k_new.stride() != v_new.stride():
         raise ValueError("k_new and v_new must share strides")
+    if out.shape != q.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} differs from q shape {tuple(q.shape)}")
     for name, t in (("q", q), ("k_new", k_new), ("out", out)):
         if t.dtype != v_cache.dtype:
             raise ValueError(f"{name} dtype differs from the caches")

@@ -236,6 +236,11 @@ def test_validation_errors(device):
         ops.decode_attention(qq, cc, max_seqlen=4, seqlen_bias=4, kernel="mfma")  # fp32
     with pytest.raises(ValueError):
         ops.decode_attention(q, cache, max_seqlen=4, seqlen_bias=4, softmax_scale=-1.0)
+    # an output smaller than q is refused on the host, before the kernel could write past it
+    with pytest.raises(ValueError, match="out shape"):
+        ops.decode_attention(q, cache, max_seqlen=4, seqlen_bias=4, out=torch.empty_like(q[:1]))
+    with pytest.raises(ValueError, match="out shape"):
+        ops.decode_attention_noalloc(q, cache, torch.empty_like(q[:, :, :4]), max_seqlen=4, seqlen_bias=4)
 
 
 # ------------------------------------------------------------- work lists ---

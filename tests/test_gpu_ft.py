@@ -250,6 +250,8 @@ def test_ft_rejections(device):
         ops.ft_attend(q[:, :3], new[:, 0], new[:, 1], k_ft, v_ft, max_position=3)  # heads not a multiple
     with pytest.raises(ValueError):
         ops.ft_attend(q, new[:, 0], new[:, 1], k_ft[:, :, :4], v_ft, max_position=3)  # K/V mismatch
+    with pytest.raises(ValueError, match="out shape"):
+        ops.ft_attend(q, new[:, 0], new[:, 1], k_ft, v_ft, max_position=3, out=torch.empty_like(q[:1]))
     longer = torch.zeros((2, 9, 2, 2, 64), dtype=dtype, device=device)
     with pytest.raises(ValueError):
         ops.ft_store(longer, k_ft, v_ft)  # more positions than capacity

@@ -239,8 +239,11 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
  *
  *   lens            host int32 [batch]
  *   items, parts    host outputs: up to items_capacity items and
- *                   parts_capacity (>= batch * head groups) partition counts;
- *                   items == NULL only sizes the plan
+ *                   parts_capacity (>= batch * head groups; batch * q_heads
+ *                   always suffices) partition counts; the device copy of
+ *                   `parts` must hold all batch * head groups of them, the
+ *                   merge reads them by (row, head group); items == NULL
+ *                   only sizes the plan
  *   n_items, max_parts   outputs: the item count and the largest partition
  *                   count (work_max_parts)
  *

@@ -314,6 +314,10 @@ def test_rows_with_hundreds_of_partitions(device, hq, hkv, d, dtype, kernel):
     lens = [20000, 3, 0, 700]
     cap = 20032
     q, cache = make(len(lens), cap, hq, hkv, d, dtype, 9, device)
+    # queries at three times the keys' scale: a row's weight then sits on few
+    # keys, so a merge stage dropped or weighted wrongly moves the output far
+    # past the tolerance (at unit scale 20,000 keys average it away)
+    q = (3 * q.float()).to(dtype)
     seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
     print(f"attend {kernel} hq={hq} hkv={hkv} d={d} {dtype}: 313 partitions", flush=True)
     live = [b for b, n in enumerate(lens) if n]
@@ -322,6 +326,7 @@ def test_rows_with_hundreds_of_partitions(device, hq, hkv, d, dtype, kernel):
         out = ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=64, kernel=kernel,
                                    lens=lens if listed else None)
         torch.cuda.synchronize()
-        err = np.abs(f64(out)[live] - ref).max()
+        # absolute error up to 1, relative above (16-bit rounding grows with the output)
+        err = (np.abs(f64(out)[live] - ref) / np.maximum(1.0, np.abs(ref))).max()
         assert err <= TOL[dtype], f"{'work list' if listed else 'grid'}: max-abs {err}"
         assert (out[2] == 0).all(), "empty row not zero"

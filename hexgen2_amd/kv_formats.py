@@ -23,8 +23,10 @@ hexkv decode path (per-sequence ``seqlens``) uses instead.
 """
 from __future__ import annotations
 
+import array
 import ctypes
 import functools
+import itertools
 import math
 from typing import Dict, List, Optional, Sequence, Tuple
 
@@ -72,10 +74,12 @@ def _layout(shape: Tuple[int, ...], stride: Tuple[int, ...], elem: int,
     return width, height, depth, r_pitch * elem, s_pitch * elem
 
 
-def _block_fields(t: torch.Tensor, split: Optional[int] = None) -> Optional[Tuple[int, ...]]:
+def _block_fields(t: torch.Tensor, split: Optional[int] = None,
+                  shape: Optional[Tuple[int, ...]] = None) -> Optional[Tuple[int, ...]]:
     """``hexkv_block`` fields (data, width, height, depth, row_pitch,
-    slice_pitch) of ``t``, or None; see ``_as_block``."""
-    lay = _layout(tuple(t.shape), t.stride(), t.element_size(), split)
+    slice_pitch) of ``t``, or None; see ``_as_block``.  ``shape``: the
+    caller's ``tuple(t.shape)``, when it has it already."""
+    lay = _layout(tuple(t.shape) if shape is None else shape, t.stride(), t.element_size(), split)
     return None if lay is None else (t.data_ptr(), *lay)
 
 
@@ -89,10 +93,11 @@ def _as_block(t: torch.Tensor, split: Optional[int] = None) -> Optional[_lib.Blo
     return None if fields is None else _lib.Block(*fields)
 
 
-def _block(t: torch.Tensor, split: Optional[int] = None) -> Tuple[Tuple[int, ...], torch.Tensor]:
+def _block(t: torch.Tensor, split: Optional[int] = None,
+           shape: Optional[Tuple[int, ...]] = None) -> Tuple[Tuple[int, ...], torch.Tensor]:
     """(block fields, tensor they describe): the tensor itself, or a
     contiguous copy when its layout has no block description."""
-    fields = _block_fields(t, split)
+    fields = _block_fields(t, split, shape)
     if fields is None:
         t = t.contiguous()
         fields = _block_fields(t, split)
@@ -101,9 +106,13 @@ def _block(t: torch.Tensor, split: Optional[int] = None) -> Tuple[Tuple[int, ...
 
 def _block_array(fields: Sequence[Tuple[int, ...]]):
     """A ``hexkv_block`` array of these fields, built in one allocation (the
-    struct is six 8-byte words: a pointer and five int64)."""
-    flat = [x for f in fields for x in f]
-    return ctypes.cast((ctypes.c_int64 * len(flat))(*flat), ctypes.POINTER(_lib.Block))
+    struct is six 8-byte words: a pointer and five int64).  The words go
+    through ``array.array``, which converts them in C: ctypes' own array
+    constructor from a list took most of the host time of a 22-layer,
+    4-shard head concatenation (~50 us for its 528 words)."""
+    words = array.array("q", list(itertools.chain.from_iterable(fields)))
+    # the ctypes view keeps `words` alive, and the cast keeps the view alive
+    return ctypes.cast((ctypes.c_int64 * len(words)).from_buffer(words), ctypes.POINTER(_lib.Block))
 
 
 def _one_dtype(tensors: Sequence[torch.Tensor], what: str) -> torch.dtype:
@@ -251,16 +260,17 @@ def batch_key_value_memory_dicts(kv_memory_dicts_list: Sequence[Dict[int, torch.
     if not keys:
         return {}
     first = [d[keys[0]] for d in dicts]
-    dtype = _one_dtype([d[k] for d in dicts for k in keys], "batch_key_value_memory_dicts")
+    grid = [[d[key] for d in dicts] for key in keys]  # [key][request]
+    dtype = _one_dtype([t for row in grid for t in row], "batch_key_value_memory_dicts")
     if any(t.dim() < 2 for t in first):
         raise ValueError("cache tensors must be [batch, positions, ...]")
-    rest = tuple(first[0].shape[2:])
-    rest_size, heads, ragged = first[0].shape[2:], [t.shape[:2] for t in first], False
-    for key in keys:
-        for i, d in enumerate(dicts):
-            shape = d[key].shape
-            if len(shape) < 2 or shape[2:] != rest_size:
-                raise ValueError(f"request {i} layer {key}: shape {tuple(shape)} does not batch with "
+    shapes = [[tuple(t.shape) for t in row] for row in grid]
+    rest = shapes[0][0][2:]
+    heads, ragged = [sh[:2] for sh in shapes[0]], False
+    for key, row in zip(keys, shapes):
+        for i, shape in enumerate(row):
+            if len(shape) < 2 or shape[2:] != rest:
+                raise ValueError(f"request {i} layer {key}: shape {shape} does not batch with "
                                  f"rows of shape {rest}")
             ragged = ragged or shape[:2] != heads[i]
     if ragged:
@@ -270,10 +280,11 @@ def batch_key_value_memory_dicts(kv_memory_dicts_list: Sequence[Dict[int, torch.
         for key in keys:
             out.update({key: batch_key_value_memory_dicts([{key: d[key]} for d in dicts], max_rows)[key]})
         return out
-    longest = max(t.shape[1] for t in first)
+    longest = max(sh[1] for sh in shapes[0])
     max_rows = longest if max_rows is None else int(max_rows)
-    seqs = sum(t.shape[0] for t in first)
+    seqs = sum(sh[0] for sh in shapes[0])
     out = torch.empty((len(keys), seqs, max_rows, *rest), dtype=dtype, device=first[0].device)
+    views = out.unbind(0)
     keep, blocks = [], []
     elem = first[0].element_size()
     width = math.prod(rest) * elem
@@ -281,21 +292,20 @@ def batch_key_value_memory_dicts(kv_memory_dicts_list: Sequence[Dict[int, torch.
     # contiguous stride
     row_dims = [d for d in range(len(rest)) if rest[d] != 1]
     row_strides = tuple(math.prod(rest[d + 1:]) for d in row_dims)
-    for key in keys:
-        for d in dicts:
-            t = d[key]
+    for row, row_shapes in zip(grid, shapes):
+        for t, shape in zip(row, row_shapes):
             st = t.stride()
-            if tuple(st[2 + d] for d in row_dims) != row_strides and t.numel():
+            if tuple(st[2 + d] for d in row_dims) != row_strides and 0 not in shape:
                 t = t.contiguous()
                 st = t.stride()
             # depth = the request's sequences, height = its positions
-            b, n = t.shape[0], t.shape[1]
+            b, n = shape[0], shape[1]
             blocks.append((t.data_ptr() if b * n else 0, width, n, b, st[1] * elem, st[0] * elem))
             keep.append(t)
-    dst = (ctypes.c_void_p * len(keys))(*[out[l].data_ptr() for l in range(len(keys))])
+    dst = (ctypes.c_void_p * len(keys))(*[v.data_ptr() for v in views])
     rc = _lib.load().hexkv_batch_pad(_block_array(blocks), len(keys), len(dicts), dst, max_rows, _stream(out))
     _lib.check(rc, "hexkv_batch_pad")
-    return {key: out[l] for l, key in enumerate(keys)}
+    return dict(zip(keys, views))
 
 
 def batch_logits_and_key_value_memory_dict(logits_list: Sequence[torch.Tensor],
@@ -343,22 +353,23 @@ def concat_dicts(list_of_dicts: Sequence[Dict[int, torch.Tensor]], dim: int = 3)
     if not -nd <= dim < nd:
         raise ValueError(f"dim {dim} out of range for {nd}-d tensors")
     dim %= nd
-    dtype = _one_dtype([d[k] for d in dicts for k in keys], "concat_dicts")
-    for key in keys:
-        shards = [d[key] for d in dicts]
-        s0 = shards[0].shape
-        for t in shards:
-            if t.dim() != nd or t.shape[:dim] != s0[:dim] or t.shape[dim + 1:] != s0[dim + 1:]:
-                raise ValueError(f"key {key}: shard shapes {[tuple(x.shape) for x in shards]} do not "
-                                 f"concatenate along dim {dim}")
-    if any(d[key].shape != d[keys[0]].shape for d in dicts for key in keys):
+    grid = [[d[key] for d in dicts] for key in keys]  # [key][shard]
+    dtype = _one_dtype([t for row in grid for t in row], "concat_dicts")
+    shapes = [[tuple(t.shape) for t in row] for row in grid]
+    for key, row in zip(keys, shapes):
+        s0 = row[0]
+        for sh in row:
+            if len(sh) != nd or sh[:dim] != s0[:dim] or sh[dim + 1:] != s0[dim + 1:]:
+                raise ValueError(f"key {key}: shard shapes {row} do not concatenate along dim {dim}")
+    if any(row != shapes[0] for row in shapes):
         # layers of different shapes: one launch per key
-        return {key: _concat_one([d[key] for d in dicts], dim) for key in keys}
-    s0 = ref.shape
-    out = torch.empty((len(keys), *s0[:dim], sum(d[keys[0]].shape[dim] for d in dicts), *s0[dim + 1:]),
+        return {key: _concat_one(row, dim) for key, row in zip(keys, grid)}
+    s0 = shapes[0][0]
+    out = torch.empty((len(keys), *s0[:dim], sum(sh[dim] for sh in shapes[0]), *s0[dim + 1:]),
                       dtype=dtype, device=ref.device)
-    _head_concat([[d[key] for d in dicts] for key in keys], [out[l] for l in range(len(keys))], dim)
-    return {key: out[l] for l, key in enumerate(keys)}
+    views = out.unbind(0)
+    _head_concat(grid, views, dim, shapes)
+    return dict(zip(keys, views))
 
 
 def _concat_one(shards: Sequence[torch.Tensor], dim: int) -> torch.Tensor:
@@ -369,17 +380,20 @@ def _concat_one(shards: Sequence[torch.Tensor], dim: int) -> torch.Tensor:
     return out
 
 
-def _head_concat(layers: Sequence[Sequence[torch.Tensor]], outs: Sequence[torch.Tensor], dim: int) -> None:
+def _head_concat(layers: Sequence[Sequence[torch.Tensor]], outs: Sequence[torch.Tensor], dim: int,
+                 shapes: Optional[Sequence[Sequence[Tuple[int, ...]]]] = None) -> None:
     """One hexkv_head_concat over every layer: rows are the indices of the
     dims before ``dim`` (however each shard folds them), a shard's row its
-    slice of the dims from ``dim`` on."""
+    slice of the dims from ``dim`` on.  ``shapes``: the shards' shapes as
+    tuples, when the caller has them."""
     keep, blocks = [], []
-    for shards in layers:
-        for t in shards:
-            if t.numel() == 0:  # no heads in this shard, or no rows at all
-                b = (0, math.prod(t.shape[dim:]) * t.element_size(), math.prod(t.shape[:dim]), 1, 0, 0)
+    for i, shards in enumerate(layers):
+        for j, t in enumerate(shards):
+            sh = tuple(t.shape) if shapes is None else shapes[i][j]
+            if 0 in sh:  # no heads in this shard, or no rows at all
+                b = (0, math.prod(sh[dim:]) * t.element_size(), math.prod(sh[:dim]), 1, 0, 0)
             else:
-                b, t = _block(t, split=dim)
+                b, t = _block(t, split=dim, shape=sh)
             keep.append(t)
             blocks.append(b)
     dst = (ctypes.c_void_p * len(layers))(*[o.data_ptr() for o in outs])

@@ -33,15 +33,18 @@ def misread_shift(n, q_scale, kv_heads, q_heads, chunk=1280, seed=0):
     return float(np.abs(oracle.attend(q, cache, [n]) - oracle.attend(q, other, [n])).max())
 
 
+# One KV head of 4 query heads (Llama-3-8B's group) keeps the host arrays
+# small; a row's statistics do not depend on how many heads there are.
+
 def test_full_size_rows_expose_a_misread_chunk():
-    # Llama-3-8B's heads (32 over 8), its longest rows; unit and doubled query scale
+    # Llama-3-8B's longest rows; unit and doubled query scale
     for scale in (1.0, 2.0):
-        assert misread_shift(8448, scale, 8, 32) > 3 * TOL_BF16
+        for seed in range(2):
+            assert misread_shift(8448, scale, 1, 4, seed=seed) > 3 * TOL_BF16
 
 
 def test_long_context_rows_need_scaled_queries():
-    # one KV head of 4 query heads keeps the CPU cost small; 70,001 positions
-    unit = [misread_shift(70001, 1.0, 1, 4, seed=s) for s in range(3)]
-    scaled = [misread_shift(70001, 3.0, 1, 4, seed=s) for s in range(3)]
+    unit = [misread_shift(70001, 1.0, 1, 4, seed=s) for s in range(2)]
+    scaled = [misread_shift(70001, 3.0, 1, 4, seed=s) for s in range(2)]
     assert min(unit) < TOL_BF16, unit
     assert min(scaled) > 3 * TOL_BF16, scaled

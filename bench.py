@@ -6,17 +6,19 @@ Llama-3-8B shape (32 layers, 8 KV / 32 query heads, head_dim 128, bf16,
 batch 64, prompt lengths U[128, 8192] seeded): pack every layer's live rows
 into the handoff buffer, unpack them into the decode cache, then 256 decode
 steps of fused KV append + single-query GQA attention over all 32 layers,
-each step one replay of a captured HIP graph after the upload of that
-step's work list (hexkv_attend_plan).  Inputs are resident in HBM before
-the timed region.
+each step one replay of its own captured HIP graph over its work list
+(planned up front with hexkv_attend_plan for the device's XCDs, split rows
+merged inside the attention kernel).  Inputs are resident in HBM before the
+timed region.
 
 Prints one JSON line: ``value`` = pack+unpack GB/s (algorithmic bytes), with
 the decode append+attend time per step, the roofline of the dominant kernel
 (decode attention) and the CPU baseline (the reference's PyTorch ops on this
-host's cores, on a bounded sample of the same workload).  Secondary figures
-outside the timed steps: ``formats`` (the legacy KV formats) and
-``ft_layout`` (the FasterTransformer cache layout), each with a ``cpu``
-entry timed the same way.
+host's cores, on a bounded sample of the same workload).  After the timed
+job, outside it: ``workloads`` -- the same measurements (fewer steps) for the
+TinyLlama-1.1B, Llama-2-7B and Llama-2-70B TP-8 shapes, each with its own
+roofline and CPU baseline -- and ``formats`` (the legacy KV formats) with
+their CPU figures.  ``--ft`` adds the FasterTransformer cache layout.
 """
 from __future__ import annotations
 
@@ -49,7 +51,7 @@ def log(msg):
 class Job:
     """Device buffers of one workload and the timed job pass."""
 
-    def __init__(self, w, device, kernel="auto", grid=False):
+    def __init__(self, w, device, kernel="auto", grid=False, single_launch=True):
         self.w = w
         self.kernel = kernel
         L, B, S = w.layers, w.batch, w.capacity
@@ -66,32 +68,49 @@ class Job:
         self.out = torch.empty((B, 1, w.q_heads, w.head_dim), dtype=w.dtype, device=device)
         self.seqlens = torch.tensor(w.lens, dtype=torch.int32, device=device)
         self.max_len = max(w.lens)
-        # Decode steps run the host-planned work list (the lengths are known
-        # here): one list per step, shared by every layer.
+        self.grid, self.single_launch = grid, single_launch
+        # Eager decode steps: one parameter block for every layer; with work
+        # lists (the lengths are known here) every step's list is planned up
+        # front, the same lists the captured graphs run.
         self.plan = ops.AttendPlan(self.q[0], self.decode_layers[0], self.out,
                                    max_seqlens=[self.max_len + t + 1 for t in range(w.decode_steps)],
-                                   seqlens=self.seqlens, kv_new=self.kv_new[0], kernel=kernel,
-                                   lens=None if grid else w.lens)
-        self.grid = grid
+                                   seqlens=self.seqlens, kv_new=self.kv_new[0], kernel=kernel)
+        self.lists = None
+        if not grid:
+            self.lists = ops.StepWorkLists(self.plan.params, w.lens, w.decode_steps, device, single_launch)
+            self.plan.reserve(self.lists.lists)
         self.kernel_name = ops.attend_kernel(self.q[0], self.decode_layers[0], kernel)
         self.positions = self.seqlens.clone()
         self.graph = None
+        # TinyLlama's 46 MB handoff fits in the 256 MB MALL: a 512 MB fill
+        # between timed steps evicts it
+        self.mall_flush = None
+        if w.pack_unpack_bytes() < (1 << 30):
+            self.mall_flush = torch.empty(512 << 20, dtype=torch.uint8, device=device)
         torch.cuda.synchronize()
 
+    @property
+    def schedule(self):
+        if self.grid:
+            return "uniform grid, split rows merged by a second kernel"
+        return ("work lists planned per step up front (hexkv_attend_plan)"
+                + (f", for {self.lists.xcds} XCDs: split rows merged in the attention kernel (one launch)"
+                   if self.lists.xcds else ", split rows merged by a second kernel"))
+
     def capture_graph(self):
-        """The all-layer decode step as one HIP graph (after an eager pass),
-        with the per-step work lists unless the bench runs the grid."""
+        """The all-layer decode step as captured HIP graphs (after an eager
+        pass): one per step over its work list, or one over the grid."""
         w = self.w
         self.graph = ops.DecodeStepGraph(list(self.q.unbind(0)), self.decode_layers, [self.out] * w.layers,
                                          list(self.kv_new.unbind(0)), self.positions,
                                          self.max_len + w.decode_steps, kernel=self.kernel,
-                                         lens=None if self.grid else w.lens)
+                                         lens=None if self.grid else w.lens, single_launch=self.single_launch)
 
-    def run_graph(self, events=None):
-        """pack -> unpack -> decode steps replayed from the captured graph
-        (each replay preceded by its step's work-list upload); records
-        (pack, unpack, step...) events."""
+    def handoff(self, events=None):
+        """pack -> unpack, recording (start, packed, unpacked) events."""
         w, ev = self.w, events
+        if self.mall_flush is not None:
+            self.mall_flush.fill_(1)
         if ev is not None:
             ev[0].record()
         ops.pack_live(self.prefill, w.lens, out=self.packed)
@@ -100,31 +119,57 @@ class Job:
         ops.unpack_live(self.packed, self.decode, w.lens)
         if ev is not None:
             ev[2].record()
+
+    def run_graph(self, events=None):
+        """pack -> unpack -> decode steps replayed from the captured graphs;
+        records (start, packed, unpacked, decoded) events.  The decode steps
+        run back to back with no event between them: an event recorded after
+        every replay put a gap of its own between the graphs (about 10 us a
+        step on this GPU), which a decode loop does not have."""
+        w, ev = self.w, events
+        self.handoff(ev)
         self.positions.copy_(self.seqlens)
         self.graph.restart()
         for t in range(w.decode_steps):
             self.graph.replay()
-            if ev is not None:
-                ev[3 + t].record()
+        if ev is not None:
+            ev[3].record()
+
+    def eager_step(self, t):
+        """Decode step t launched layer by layer from the host."""
+        w = self.w
+        if self.lists is not None:
+            self.plan.fix_work_list(self.lists[t])
+        for l in range(w.layers):
+            self.plan(self.q[l], self.decode_layers[l], self.out, self.kv_new[l], t, self.max_len + t + 1)
 
     def run(self, events=None):
         """pack -> unpack -> decode steps launched eagerly, layer by layer;
-        records (pack, unpack, step...) events."""
-        w = self.w
-        ev = events
-        if ev is not None:
-            ev[0].record()
-        ops.pack_live(self.prefill, w.lens, out=self.packed)
-        if ev is not None:
-            ev[1].record()
-        ops.unpack_live(self.packed, self.decode, w.lens)
-        if ev is not None:
-            ev[2].record()
+        records (start, packed, unpacked, decoded) events."""
+        w, ev = self.w, events
+        self.handoff(ev)
         for t in range(w.decode_steps):
-            for l in range(w.layers):
-                self.plan(self.q[l], self.decode_layers[l], self.out, self.kv_new[l], t, self.max_len + t + 1)
-            if ev is not None:
-                ev[3 + t].record()
+            self.eager_step(t)
+        if ev is not None:
+            ev[3].record()
+
+    def decode_mall_busted(self):
+        """Average µs of one graph-replayed decode step when the MALL is
+        evicted before every step (the fill outside the timed step)."""
+        w = self.w
+        self.handoff()
+        self.positions.copy_(self.seqlens)
+        self.graph.restart()
+        total = 0.0
+        for t in range(w.decode_steps):
+            self.mall_flush.fill_(1)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            self.graph.replay()
+            e1.record()
+            e1.synchronize()
+            total += e0.elapsed_time(e1)
+        return total * 1e3 / w.decode_steps  # (each step between its own events)
 
     def traffic_probe(self):
         """A short fixed dispatch sequence for hardware-counter runs
@@ -149,8 +194,7 @@ class Job:
         log("pack, unpack, one decode step")
         ops.pack_live(self.prefill, w.lens, out=self.packed)
         ops.unpack_live(self.packed, self.decode, w.lens)
-        for l in range(w.layers):
-            self.plan(self.q[l], self.decode_layers[l], self.out, self.kv_new[l], 0, self.max_len + 1)
+        self.eager_step(0)
         torch.cuda.synchronize()
         log("probe done")
 
@@ -422,72 +466,50 @@ def cpu_baseline(w, job, budget_s):
             "pack_s": round(t1 - t0, 3), "unpack_s": round(t2 - t1, 3), "single_thread": single}
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", default="llama3-8b", choices=WORKLOADS)
-    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode work")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-verify", action="store_true")
-    ap.add_argument("--no-formats", action="store_true", help="skip the legacy-format figures")
-    ap.add_argument("--kernel", default="auto", choices=("auto", "valu", "mfma"),
-                    help="attention kernel (auto: the library's choice for the workload)")
-    ap.add_argument("--grid", action="store_true",
-                    help="decode attention over the library's uniform partitions instead of the work list")
-    ap.add_argument("--traffic-probe", action="store_true",
-                    help="run only the short dispatch sequence for hardware-counter runs")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the KV path here runs prefill and decode on one "
-              "MI355X; run it with --gpus 1", file=sys.stderr)
-        sys.exit(2)
-    device = torch.device("cuda", 0)
-    w = workload(args.workload)
-    log(f"workload {w.describe()}")
-    job = Job(w, device, args.kernel, grid=args.grid)
-    log(f"buffers ready; attention kernel {job.kernel_name}")
-    if args.traffic_probe:
-        job.traffic_probe()
-        del job
-        torch.cuda.empty_cache()
-        Job.formats_traffic_probe(device)
-        return
+SECONDARY = ("tinyllama-1.1b", "llama2-7b", "llama2-70b-tp8")
+
+
+def measure(w, device, args, steps, warmup, cpu_budget):
+    """Build the workload's job, check its full-size handoff, and time
+    ``steps`` job passes after ``warmup`` (each pass: pack, unpack, every
+    decode step as one graph replay); then the eager decode, the
+    MALL-evicted decode (workloads whose handoff fits in the MALL) and the
+    CPU baseline.  Returns (result fields, wall seconds of the timed passes)."""
+    job = Job(w, device, args.kernel, grid=args.grid, single_launch=not args.two_launch)
+    log(f"{w.name}: buffers ready; attention kernel {job.kernel_name}; {job.schedule}")
     if not args.no_verify:
         job.verify()
-        log("full-size pack/unpack round trip verified")
-
-    n_ev = 3 + w.decode_steps
-    job.run()  # eager pass: loads every kernel before the graph is captured
+        log(f"{w.name}: full-size pack/unpack round trip verified")
+    n_ev = 4
+    job.run()  # eager pass: loads every kernel before the graphs are captured
     torch.cuda.synchronize()
     job.capture_graph()
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         job.run_graph()
     torch.cuda.synchronize()
-    log("warmup done")
-
-    pu_times, pack_times, decode_steps_ms, wall = [], [], [], []
+    log(f"{w.name}: warmup done")
+    pu_times, pack_times, decode_ms = [], [], []
     torch.cuda.synchronize()
     t_start = time.perf_counter()
-    for k in range(args.steps):
+    for k in range(steps):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
         job.run_graph(ev)
         torch.cuda.synchronize()
         pack_times.append(ev[0].elapsed_time(ev[1]))
         pu_times.append(ev[0].elapsed_time(ev[2]))
-        decode_steps_ms.extend(ev[2 + t].elapsed_time(ev[3 + t]) for t in range(w.decode_steps))
-        log(f"step {k}: pack+unpack {pu_times[-1]:.3f} ms, decode {ev[2].elapsed_time(ev[-1]):.1f} ms")
+        decode_ms.append(ev[2].elapsed_time(ev[3]))
+        log(f"{w.name} step {k}: pack+unpack {pu_times[-1]:.3f} ms, decode {decode_ms[-1]:.1f} ms")
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
 
     pu_ms = statistics.median(pu_times)
     pu_gbs = w.pack_unpack_bytes() / (pu_ms * 1e-3) / 1e9
-    decode_total_ms = sum(decode_steps_ms) / args.steps
+    decode_total_ms = sum(decode_ms) / steps
     decode_us_step = decode_total_ms / w.decode_steps * 1e3
     decode_gbs = w.decode_bytes() / (decode_total_ms * 1e-3) / 1e9
     launch_bytes = w.decode_bytes() / (w.layers * w.decode_steps)
     attend_us = decode_total_ms * 1e3 / (w.layers * w.decode_steps)
+    achieved = launch_bytes / (attend_us * 1e-6) / 1e9
     # HBM bytes per attention call: not measured in this run (hardware
     # counters need a rocprofv3 --pmc run of their own).  Derived from the
     # committed counter runs (FETCH_SIZE + WRITE_SIZE at decode step 0,
@@ -498,9 +520,97 @@ def main():
         traffic_ratio = json.loads(TRAFFIC_FILE.read_text()).get(w.name, {}).get("traffic_over_algorithmic")
         if traffic_ratio:
             traffic = int(traffic_ratio * launch_bytes)
+    kernels = f"attend_{job.kernel_name}_kernel" + (" + combine_kernel" if job.grid or not job.lists.xcds else "")
+    r = {
+        "pack_unpack_gbs": round(pu_gbs, 1),
+        "pack_unpack_ms": round(pu_ms, 3),
+        "pack_unpack_hbm_frac": round(pu_gbs / HBM_PEAK_GBS, 4),
+        "pack_ms": round(statistics.median(pack_times), 3),
+        "decode_append_attend_us_per_step": round(decode_us_step, 1),
+        "decode_gbs": round(decode_gbs, 1),
+        "decode_hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "kernel": f"one hexkv_attend call = {kernels} (fused append+attend, one layer)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "traffic_source": (f"derived: committed PMC ratio {traffic_ratio} (profiles/traffic.json, decode "
+                               "step 0) x this run's algorithmic bytes per call") if traffic else None,
+            "bytes_per_launch": int(launch_bytes),
+            "avg_launch_us": round(attend_us, 2),
+            "timing": "HIP events on the launch stream around the decode phase of every timed pass (all "
+                      "its graph replays back to back); avg_launch_us = decode time / (layers x steps), i.e. "
+                      "the attention call of one layer with its share of the gaps between launches",
+        },
+    }
+    # Outside the timed passes: the same decode steps launched eagerly, layer
+    # by layer, from the host (host gaps included).
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+    job.run(ev)
+    torch.cuda.synchronize()
+    eager_ms = ev[2].elapsed_time(ev[3])
+    r["decode_eager_us_per_step"] = round(eager_ms / w.decode_steps * 1e3, 1)
+    log(f"{w.name}: eager decode {eager_ms:.1f} ms")
+    if job.mall_flush is not None:
+        r["mall"] = ("pack+unpack timed after a 512 MB fill evicts the 256 MB MALL; the decode steps run "
+                     "back to back with their working set MALL-resident, decode_mall_evicted_us_per_step "
+                     "fills before every step")
+        r["decode_mall_evicted_us_per_step"] = round(job.decode_mall_busted(), 1)
+    if cpu_budget is not None:
+        log(f"{w.name}: cpu baseline")
+        r["cpu_baseline"] = cpu_baseline(w, job, cpu_budget)
+    r["config"] = {**w.describe(), "attention_kernel": job.kernel_name, "attention_schedule": job.schedule}
+    del job
+    torch.cuda.empty_cache()
+    return r, elapsed
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="llama3-8b", choices=WORKLOADS,
+                    help="the timed workload (the other GPU workloads follow it unless --no-secondary)")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline decode work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--no-formats", action="store_true", help="skip the legacy-format figures")
+    ap.add_argument("--no-secondary", action="store_true", help="time only --workload")
+    ap.add_argument("--ft", action="store_true", help="add the FasterTransformer-layout figures")
+    ap.add_argument("--kernel", default="auto", choices=("auto", "valu", "mfma"),
+                    help="attention kernel (auto: the library's choice for the workload)")
+    ap.add_argument("--grid", action="store_true",
+                    help="decode attention over the library's uniform partitions instead of work lists")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="work lists whose split rows a second kernel merges (not planned for the XCDs)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the short dispatch sequence for hardware-counter runs")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the KV path here runs prefill and decode on one "
+              "MI355X; run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    w = workload(args.workload)
+    log(f"workload {w.describe()}")
+    if args.traffic_probe:
+        job = Job(w, device, args.kernel, grid=args.grid, single_launch=not args.two_launch)
+        log(f"buffers ready; attention kernel {job.kernel_name}; {job.schedule}")
+        job.traffic_probe()
+        del job
+        torch.cuda.empty_cache()
+        Job.formats_traffic_probe(device)
+        return
+
+    head, elapsed = measure(w, device, args, args.steps, args.warmup,
+                            None if args.no_cpu_baseline else args.cpu_budget)
     result = {
         "metric": METRIC,
-        "value": round(pu_gbs, 1),
+        "value": head["pack_unpack_gbs"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -511,60 +621,38 @@ def main():
         "vs_baseline": None,
         "dtype": str(w.dtype).split(".")[-1].replace("bfloat16", "bf16").replace("float16", "fp16"),
         "data": "synthetic (seeded N(0,1) K/V, seeded ragged lengths)",
-        "config": {**w.describe(), "attention_kernel": job.kernel_name,
-                   "attention_schedule": "uniform grid" if args.grid else "work list (hexkv_attend_plan)",
-                   "parallelism": "single GPU (prefill and decode share it)"},
-        "pack_unpack_ms": round(pu_ms, 3),
-        "pack_unpack_hbm_frac": round(pu_gbs / HBM_PEAK_GBS, 4),
-        "pack_ms": round(statistics.median(pack_times), 3),
-        "decode_append_attend_us_per_step": round(decode_us_step, 1),
-        "decode_gbs": round(decode_gbs, 1),
-        "decode_hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
-        "roofline": {
-            "kernel": f"one hexkv_attend call = attend_{job.kernel_name}_kernel + combine_kernel "
-                      "(fused append+attend, one layer)",
-            "bound": "hbm",
-            "achieved": round(launch_bytes / (attend_us * 1e-6) / 1e9, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(launch_bytes / (attend_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "traffic_source": (f"derived: committed PMC ratio {traffic_ratio} (profiles/traffic.json, decode "
-                               "step 0) x this run's algorithmic bytes per call") if traffic else None,
-            "bytes_per_launch": int(launch_bytes),
-            "avg_launch_us": round(attend_us, 2),
-            "timing": "HIP events on the launch stream around every timed decode step (one graph replay "
-                      "after its work-list upload); avg_launch_us = decode time / (layers x steps), i.e. the "
-                      "attention kernel plus its combine kernel, the upload's share included",
-        },
-        "cpu_baseline": None,
+        "config": {**head.pop("config"), "parallelism": "single GPU (prefill and decode share it)"},
+        "cpu_baseline": head.pop("cpu_baseline", None),
     }
-    # Secondary figure, outside the timed steps: the same job with every
-    # layer's call launched eagerly from the host (host gaps included).
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    job.run(ev)
-    torch.cuda.synchronize()
-    eager_ms = sum(ev[2 + t].elapsed_time(ev[3 + t]) for t in range(w.decode_steps))
-    result["decode_eager_us_per_step"] = round(eager_ms / w.decode_steps * 1e3, 1)
-    log(f"eager decode {eager_ms:.1f} ms")
-    if not args.no_cpu_baseline:
-        log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(w, job, args.cpu_budget)
+    result.update(head)
+    if not args.no_secondary:
+        # the other GPU configurations, outside the timed job: a few passes each
+        steps, warmup = max(1, min(args.steps, 5)), min(args.warmup, 2)
+        cpu_budget = None if args.no_cpu_baseline else min(args.cpu_budget, 5.0)
+        result["workloads"] = {}
+        for name in SECONDARY:
+            if name == w.name:
+                continue
+            r, wall = measure(workload(name), device, args, steps, warmup, cpu_budget)
+            r["steps"], r["warmup"], r["ms_per_step"] = steps, warmup, round(wall * 1e3 / steps, 2)
+            result["workloads"][name] = r
+            log(f"{name}: {r['pack_unpack_gbs']} GB/s pack+unpack, {r['decode_append_attend_us_per_step']} us "
+                f"per decode step, attention call {r['roofline']['avg_launch_us']} us ({r['roofline']['frac']})")
     if not args.no_formats:
-        del job
-        torch.cuda.empty_cache()
         result["formats"] = measure_formats(device)
         log(f"legacy formats {result['formats']}")
-        result["ft_layout"] = measure_ft(device)
-        log(f"FT layout {result['ft_layout']}")
+        if args.ft:
+            result["ft_layout"] = measure_ft(device)
+            log(f"FT layout {result['ft_layout']}")
         if not args.no_cpu_baseline:
             cores = result["cpu_baseline"]["cores"]
             for name, cpu in cpu_formats(cores).items():
                 result["formats"][name]["cpu"] = cpu
-            store_cpu, attend_cpu = cpu_ft(cores, workload("llama3-8b"))
-            result["ft_layout"]["ft_store"]["cpu"] = store_cpu
-            result["ft_layout"]["ft_attend"]["cpu"] = attend_cpu
-            log(f"CPU formats and FT {result['formats']} {result['ft_layout']}")
+            if args.ft:
+                store_cpu, attend_cpu = cpu_ft(cores, workload("llama3-8b"))
+                result["ft_layout"]["ft_store"]["cpu"] = store_cpu
+                result["ft_layout"]["ft_attend"]["cpu"] = attend_cpu
+            log("CPU formats done")
     print(json.dumps(result), flush=True)
 
 

@@ -22,8 +22,15 @@ EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "h
            "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
            "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend",
-           "hexkv_attend_noalloc", "hexkv_attend_plan", "hexkv_attend_plan_chunk")
+           "hexkv_attend_noalloc", "hexkv_attend_plan", "hexkv_attend_plan_chunk", "hexkv_device_status",
+           "hexkv_device_xcds")
 NOALLOC_SCRATCH_BYTES = 32 << 20
+# Arrival counters at the front of every attention workspace (zero them once).
+ATTEND_COUNTER_BYTES = 256 << 10
+ATTEND_COUNTER_WORDS = ATTEND_COUNTER_BYTES // 8  # one 64-bit counter per (row, head group)
+# Device status flags (hexkv_device_status).
+STATUS_APPEND_SKIPPED, STATUS_LENGTH_CLAMPED, STATUS_PLACEMENT, STATUS_DISPATCH = 1, 2, 4, 8
+STATUS_ERRORS = STATUS_APPEND_SKIPPED | STATUS_LENGTH_CLAMPED | STATUS_PLACEMENT
 
 
 class AttendParams(ctypes.Structure):
@@ -41,6 +48,7 @@ class AttendParams(ctypes.Structure):
         ("kv_new", ctypes.c_void_p), ("partition", ctypes.c_int), ("kernel", ctypes.c_int),
         ("work_items_dev", ctypes.c_void_p), ("work_parts_dev", ctypes.c_void_p),
         ("n_work_items", ctypes.c_int32), ("work_max_parts", ctypes.c_int32),
+        ("work_xcds", ctypes.c_int32), ("lengths_out_dev", ctypes.c_void_p),
     ]
 
 
@@ -99,6 +107,10 @@ def load() -> ctypes.CDLL:
     lib.hexkv_version.argtypes = []
     lib.hexkv_last_error.restype = ctypes.c_char_p
     lib.hexkv_last_error.argtypes = []
+    lib.hexkv_device_status.restype = ci
+    lib.hexkv_device_status.argtypes = [ctypes.POINTER(ctypes.c_uint32), ci, vp]
+    lib.hexkv_device_xcds.restype = ci
+    lib.hexkv_device_xcds.argtypes = [ctypes.POINTER(ctypes.c_int32)]
     for name in ("hexkv_pack", "hexkv_unpack"):
         fn = getattr(lib, name)
         fn.restype = ci

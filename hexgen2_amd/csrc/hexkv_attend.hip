@@ -44,15 +44,21 @@
 // streaming loop, and the workgroup owning it writes it to the cache.
 //
 // A row with one partition writes its normalised output directly.  With
-// several, each partition stores (unnormalised o, max, sum) to the workspace
-// and `combine_kernel`, launched next on the same stream, merges them.  (A
-// last-arriver merge inside the attention kernel needs an agent-scope release
-// per workgroup, which on this part writes back the whole L2 of the XCD and
-// serialises: measured 2-20x slower than the second launch.  With
-// write-through partial stores and an arrival counter instead of the release
-// it still lost: the store wait, the counter round trip and the reload of
-// the partials sit on the last items' path, 178.8 against 176.1 us per
-// Llama-3-8B layer and 16.5 against 14.4 at the Llama-2-70B TP-8 share.)
+// several, each partition stores (unnormalised o, max, sum) to the workspace,
+// and the partials are merged in one of two ways:
+//   * XCD-local, in the attention kernel (work lists planned for the device's
+//     XCDs, work_xcds > 0): every item of a split segment sits at one index
+//     modulo the XCD count, and workgroups reach the XCDs round-robin by
+//     index, so all of them run on one XCD and share its L2.  Each stores its
+//     partial, waits for the stores (s_waitcnt vmcnt(0): they are in that
+//     L2), and counts its arrival with an L2 atomic; the last one drops its
+//     L1 lines (buffer_inv sc0), reads the partials from the L2, writes the
+//     output and resets the counter.  No L2 writeback is needed.  (The
+//     device-wide form -- an agent-scope release per workgroup, which writes
+//     back the XCD's whole L2 -- measured 17x slower than the XCD-local one
+//     in an in-bounds probe, and with partials spread over XCDs the plain
+//     form reads stale data: the XCDs' L2s are not coherent.)
+//   * otherwise `combine_kernel`, launched next on the same stream.
 #include "hexkv_common.h"
 
 #include <algorithm>
@@ -100,6 +106,12 @@ struct AttendArgs {
   const int32_t *seg_parts;
   int32_t n_groups;
   int32_t rows;  // query rows (batch * q_len)
+  // XCD-local merge (work lists planned for n_xcd XCDs): arrival counters
+  // [rows * n_groups], zero between calls; nullptr: combine_kernel merges.
+  uint64_t *seg_count;
+  int32_t n_xcd;
+  int32_t *lengths_out;  // work lists with kv_new: row b's new length, or nullptr
+  unsigned int *status;  // HEXKV_STATUS_* word of this device, or nullptr
   // FasterTransformer cache layouts (hexkv_ft_attend only): K is
   // [batch][kv_heads][D / pack][capacity][pack] (one 16-byte chunk of D per
   // position), V is [batch][kv_heads][capacity][D]; strides in bytes.  The
@@ -117,7 +129,7 @@ struct AttendArgs {
 
 // Number of keys query row (b, t) attends to; *pos_new = cache position of the
 // fused-append row (or -1).
-__device__ __forceinline__ int row_length(const AttendArgs &a, int b, int t, int *pos_new) {
+__device__ __forceinline__ int row_length(const AttendArgs &a, int b, int t, int *pos_new, bool *clamped) {
   int len = (a.seqlens ? a.seqlens[b] : 0) + a.bias;
   *pos_new = -1;
   if (a.kv_new) {
@@ -127,7 +139,8 @@ __device__ __forceinline__ int row_length(const AttendArgs &a, int b, int t, int
   if (a.causal) len = len - a.q_len + t + 1;
   // Lengths come from device memory: clamp to the host bound that sized the
   // grid and the workspace (max_seqlen <= capacity is checked on the host),
-  // so no row can reach past either.
+  // so no row can reach past either, and report it.
+  *clamped = len > a.max_seqlen;
   if (len > a.max_seqlen) len = a.max_seqlen;
   return len;
 }
@@ -139,7 +152,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // when has_new, the last one (pos_new) from kv_new.
 struct Work {
   int row, b, t, len, part, p0, n, n_cache, nparts, qh0, hk, pos_new;
-  bool has_new, writer;
+  bool has_new, writer, clamped;
 };
 
 // Fills `w`; returns false when the workgroup has nothing to do (after
@@ -147,16 +160,16 @@ struct Work {
 template <typename T, int D, int G>
 __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
   int hg;
+  w.clamped = false;
   if (a.items) {
     const hexkv_work_item it = a.items[blockIdx.x];
     // Items come from device memory: one naming a row, head group, partition
     // or positions outside this call's geometry does nothing.
-    if (static_cast<unsigned>(it.row) >= static_cast<unsigned>(a.rows) ||
-        static_cast<unsigned>(it.head_group) >= static_cast<unsigned>(a.n_groups) ||
-        static_cast<unsigned>(it.part) >= static_cast<unsigned>(a.max_parts) || it.parts < 1 ||
-        it.parts > a.max_parts || it.first < 0 || it.count < 0 || it.len > a.max_seqlen ||
-        it.first + it.count > it.len)
-      return false;
+    if (!work_item_fits(it, a.rows, a.n_groups, a.max_parts, a.max_seqlen)) return false;
+    // The item holding a row's last position of head group 0 records the
+    // row's new length (work lists read no seqlens, so this may alias them).
+    if (a.lengths_out && threadIdx.x == 0 && it.head_group == 0 && it.len > 0 && it.count == it.len - it.first)
+      a.lengths_out[it.row] = it.len;
     w.row = w.b = it.row;
     w.t = 0;
     hg = it.head_group;
@@ -170,7 +183,7 @@ __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
     w.row = blockIdx.z;
     w.b = w.row / a.q_len;
     w.t = w.row - w.b * a.q_len;
-    w.len = row_length(a, w.b, w.t, &w.pos_new);
+    w.len = row_length(a, w.b, w.t, &w.pos_new, &w.clamped);
     hg = blockIdx.y;
     w.part = blockIdx.x;
     w.p0 = w.part * a.part;
@@ -200,8 +213,95 @@ __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
   return true;
 }
 
+// Largest partition count a single-launch merge takes (the host sends calls
+// with more to combine_kernel): one wave holds a head's (max, sum) pairs.
+constexpr int kMergeMaxParts = 64;  // also keeps each XCD's 8-bit arrival count from overflowing
+
+// The XCD-local merge of a split segment (row, head group qh0 / G), after
+// this workgroup stored its partial: count the arrival; the last of the
+// segment's w.nparts items reads every partial from the XCD's L2 and writes
+// the normalised output, parts in index order (the result does not depend
+// on which item arrives last).  The partial loads of the first kDepth parts
+// go out together with the (max, sum) loads, so the merge waits for about
+// one L2 round trip: each thread owns VPT consecutive outputs of the G x D
+// block (one VPT-float load per part), and the waves turn the (max, sum)
+// pairs into per-part weights in LDS meanwhile.
+template <typename T, int D, int G>
+__device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w) {
+  constexpr int OUT = G * D;
+  static_assert(OUT <= 4 * kAttThreads, "one pass over the segment's outputs");
+  constexpr int VPT = OUT >= 4 * kAttThreads ? 4 : OUT >= 2 * kAttThreads ? 2 : 1;
+  constexpr int kDepth = 16;
+  typedef float vecf __attribute__((ext_vector_type(VPT)));
+  __shared__ int s_last;
+  __shared__ float2 s_ml[G][kMergeMaxParts];
+  __shared__ float s_w[G][kMergeMaxParts];
+  // Every wave's partial stores have reached the L2 before the arrival counts.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // One 64-bit counter per segment, an 8-bit arrival count per XCD: the last
+  // arrival sees whether every part ran on its own XCD (the L2 it reads).
+  uint64_t *count = a.seg_count + static_cast<int64_t>(w.row) * a.n_groups + w.qh0 / G;
+  if (threadIdx.x == 0) {
+    const int x = xcd_id() & 7;
+    const uint64_t mine = UINT64_C(1) << (8 * x);
+    const uint64_t old = __hip_atomic_fetch_add(count, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int arrived = static_cast<int>((old * UINT64_C(0x0101010101010101)) >> 56);  // byte sum (< 256)
+    s_last = arrived == w.nparts - 1;
+    if (s_last && old + mine != static_cast<uint64_t>(w.nparts) << (8 * x))
+      raise_status(a.status, HEXKV_STATUS_PLACEMENT);
+    if (static_cast<unsigned>(x) % a.n_xcd != blockIdx.x % a.n_xcd) raise_status(a.status, HEXKV_STATUS_DISPATCH);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // Drop this CU's L1 lines so the partials come from the L2.
+  asm volatile("buffer_inv sc0" ::: "memory");
+  const int n = w.nparts, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t slot0 = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0) * a.max_parts;
+  const int i0 = tid * VPT;  // first output of this thread, (g, d) = (i0 / D, i0 % D)
+  const bool owner = i0 < OUT;
+  const int g = owner ? i0 / D : 0, d = i0 - g * D;
+  const float *o = a.ws_o + (slot0 + static_cast<int64_t>(g) * a.max_parts) * D + d;
+  vecf ov[kDepth];
+#pragma unroll
+  for (int u = 0; u < kDepth; ++u)
+    ov[u] = owner && u < n ? *reinterpret_cast<const vecf *>(o + static_cast<int64_t>(u) * D) : vecf{};
+  for (int j = tid; j < G * n; j += kAttThreads) {
+    const int jg = j / n, jp = j - jg * n;
+    s_ml[jg][jp] = *reinterpret_cast<const float2 *>(a.ws_ml + (slot0 + static_cast<int64_t>(jg) * a.max_parts + jp) * 2);
+  }
+  __syncthreads();
+  // weights w_p = 2^(m_p - max m) / sum_p 2^(m_p - max m) l_p, one head per wave
+  for (int h = wave; h < G; h += kAttWaves) {
+    const float2 ml = lane < n ? s_ml[h][lane] : float2{kNoScore, 0.f};
+    const float mx = wave_max(ml.x);
+    const float e = lane < n ? fast_exp2(ml.x - mx) : 0.f;
+    const float total = sum_from<1>(e * ml.y);
+    if (lane < n) s_w[h][lane] = e / total;
+  }
+  __syncthreads();
+  if (!owner) return;
+  vecf acc{};
+#pragma unroll
+  for (int u = 0; u < kDepth; ++u)
+    if (u < n) acc += s_w[g][u] * ov[u];
+  for (int p0 = kDepth; p0 < n; p0 += kDepth) {
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u)
+      ov[u] = p0 + u < n ? *reinterpret_cast<const vecf *>(o + static_cast<int64_t>(p0 + u) * D) : vecf{};
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u)
+      if (p0 + u < n) acc += s_w[g][p0 + u] * ov[u];
+  }
+  T *out = static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D + i0;
+#pragma unroll
+  for (int v = 0; v < VPT; ++v) out[v] = Elem<T>::from_float(acc[v]);
+  if (tid == 0) __hip_atomic_store(count, static_cast<uint64_t>(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Merges the 4 waves' (max, sum, o) held in LDS into this partition's result:
-// the normalised output for a single-partition row, else a workspace partial.
+// the normalised output for a single-partition row, else a workspace partial
+// (merged here, XCD-locally, when the call has arrival counters).
 template <typename T, int D, int G>
 __device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
                                             const float (*s_acc)[G][D], const float (*s_m)[G],
@@ -230,6 +330,10 @@ __device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
         a.ws_ml[slot * 2 + 1] = sum;
       }
     }
+  }
+  if (w.clamped && threadIdx.x == 0) raise_status(a.status, HEXKV_STATUS_LENGTH_CLAMPED);
+  if constexpr (G * D <= 4 * kAttThreads) {  // the host merges larger blocks with combine_kernel
+    if (w.nparts > 1 && a.seg_count) merge_split<T, D, G>(a, w);
   }
 }
 
@@ -963,7 +1067,8 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
         nparts = min(a.seg_parts[row * a.n_groups + h / G], a.max_parts);
       } else {
         int pos_new;
-        const int len = row_length(a, b, t, &pos_new);
+        bool clamped;
+        const int len = row_length(a, b, t, &pos_new, &clamped);
         nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
       }
       if (nparts <= 1) return;  // written by the attention kernel
@@ -1020,7 +1125,8 @@ __global__ __launch_bounds__(kAttThreads) void combine_kernel(const AttendArgs a
     nparts = min(a.seg_parts[row * a.n_groups + h / G], a.max_parts);
   } else {
     int pos_new;
-    const int len = row_length(a, b, t, &pos_new);
+    bool clamped;
+    const int len = row_length(a, b, t, &pos_new, &clamped);
     nparts = len > 0 ? (len + a.part - 1) / a.part : 0;
   }
   if (nparts <= 1) return;
@@ -1120,13 +1226,20 @@ static int64_t max_parts_of(const hexkv_attend_params *p, int part) {
   return std::max<int64_t>(1, (p->max_seqlen + part - 1) / part);
 }
 
-// Workspace: the partial outputs [rows][q_heads][max_parts][D], then their
-// (max, sum) pairs [rows][q_heads][max_parts][2], all fp32.
+// Arrival counters of the XCD-local merge at the front of every workspace
+// (one 64-bit word per (row, head group) segment), whatever the call's mode,
+// so that one workspace serves calls of either mode.
+constexpr int64_t kCounterWords = HEXKV_ATTEND_COUNTER_BYTES / sizeof(uint64_t);
+
+// Workspace: the arrival counters, then the partial outputs
+// [rows][q_heads][max_parts][D], then their (max, sum) pairs
+// [rows][q_heads][max_parts][2], all fp32.
 static size_t workspace_bytes(const hexkv_attend_params *p, int part) {
   const int64_t max_parts = max_parts_of(p, part);
   if (max_parts <= 1) return 0;
   const int64_t rows = static_cast<int64_t>(p->batch) * p->q_len;
-  return static_cast<size_t>(rows * p->q_heads * max_parts * (p->head_dim + 2)) * sizeof(float);
+  return HEXKV_ATTEND_COUNTER_BYTES +
+         static_cast<size_t>(rows * p->q_heads * max_parts * (p->head_dim + 2)) * sizeof(float);
 }
 
 static int validate(const hexkv_attend_params *p) {
@@ -1158,6 +1271,10 @@ static int validate(const hexkv_attend_params *p) {
     return fail(HEXKV_EINVAL, "hexkv_attend: unknown kernel %d", p->kernel);
   if (p->kernel == HEXKV_KERNEL_MFMA && (p->dtype == HEXKV_F32 || p->head_dim < 64))
     return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the MFMA kernel takes float16/bfloat16 with head_dim >= 64");
+  if (p->work_xcds < 0 || p->work_xcds > 64) return fail(HEXKV_EINVAL, "hexkv_attend: work_xcds outside [0, 64]");
+  if (p->lengths_out_dev && (!p->work_items_dev || !p->kv_new))
+    return fail(HEXKV_EINVAL, "hexkv_attend: lengths_out_dev needs a work list and kv_new");
+  if (p->batch == 0) return HEXKV_OK;  // nothing to launch, with or without a work list
   if (p->work_items_dev) {
     if (p->n_work_items < 1 || !p->work_parts_dev || p->work_max_parts < 1 || p->work_max_parts > 65535)
       return fail(HEXKV_EINVAL, "hexkv_attend: a work list needs n_work_items >= 1, work_parts_dev and "
@@ -1166,8 +1283,15 @@ static int validate(const hexkv_attend_params *p) {
       return fail(HEXKV_EINVAL, "hexkv_attend: work_items_dev must be 16-byte aligned, work_parts_dev 4-byte");
     if (p->q_len != 1 || p->causal)
       return fail(HEXKV_EINVAL, "hexkv_attend: a work list is for decode rows (q_len 1, not causal)");
+    if (p->work_xcds > 0 &&
+        static_cast<int64_t>(p->batch) * (p->q_heads / kernel_group(p->q_heads / p->kv_heads)) > kCounterWords)
+      return fail(HEXKV_EINVAL, "hexkv_attend: the single-launch merge counts at most %lld (row, head group) "
+                                "segments; use work_xcds 0", static_cast<long long>(kCounterWords));
+  } else if (p->work_xcds > 0) {
+    return fail(HEXKV_EINVAL, "hexkv_attend: work_xcds is for work lists");
   }
-  if (p->batch == 0) return HEXKV_OK;
+  if (p->lengths_out_dev && (reinterpret_cast<uintptr_t>(p->lengths_out_dev) & 3u))
+    return fail(HEXKV_EINVAL, "hexkv_attend: lengths_out_dev must be 4-byte aligned");
   if (!p->q || !p->cache || !p->out) return fail(HEXKV_EINVAL, "hexkv_attend: null tensor");
   const int vec = 16 / elem_size(p->dtype);
   if (!aligned16(p->q) || !aligned16(p->cache) || (p->kv_new && !aligned16(p->kv_new)))
@@ -1200,10 +1324,12 @@ constexpr int slots() {
 // share: 16.0 vs 23.8 us per layer at the best partition of each; TinyLlama:
 // 10.6 vs 11.9); the VALU kernel otherwise (Llama-3-8B, group 4: 176.4 vs
 // 180.6; Llama-2-7B, group 1: 34.8 vs 38.1).
+// head_dim 256 stays on the VALU kernel: the MFMA kernel's accumulators spill
+// to scratch there.
 static bool use_mfma(const hexkv_attend_params *p, int G) {
   if (p->kernel == HEXKV_KERNEL_MFMA) return true;
   if (p->kernel == HEXKV_KERNEL_VALU) return false;
-  return p->dtype != HEXKV_F32 && p->head_dim >= 64 && G >= 8;
+  return p->dtype != HEXKV_F32 && p->head_dim >= 64 && p->head_dim <= 128 && G >= 8;
 }
 
 // Which attention kernel a launch runs.
@@ -1219,7 +1345,7 @@ static void launch(const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
   } else {
     attend_valu_kernel<T, D, G, slots<T, D, G>()><<<grid, kAttThreads, 0, s>>>(a);
   }
-  if (a.max_parts > 1) {
+  if (a.max_parts > 1 && !a.seg_count) {
     const dim3 cgrid(a.q_heads, a.rows);
     constexpr int SL = kAttThreads / D >= 1 ? kAttThreads / D : 1;
     if (a.max_parts <= 8 * SL) combine_kernel<T, D, G, 8><<<cgrid, kAttThreads, 0, s>>>(a);
@@ -1272,8 +1398,17 @@ namespace hexkv {
 // on HBM-resident data, 36.5 at 1280; Llama-3-8B, 2.0 M: 170.3-170.9 us at
 // 1280 against 173.0-173.2 at 1024, 179 for the grid and 179.6 at 512,
 // over three boxes).
-static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest) {
+//
+// Planned for the XCDs (split segments merged in the attention kernel, no
+// second launch), calls below 4 MB are split too, in pieces of about a
+// twelfth of the longest row (64 positions at least): TinyLlama's 577-640
+// positions as 10 items of 64 per segment, 6.7 us per call against 9.1 for
+// one item per segment (7.2 at 128 positions, 7.7 at 192, 8.3 at 256;
+// HBM-resident A/B in one process).
+static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest, bool xcd_merge) {
   const int64_t bytes = positions * row_bytes;
+  if (bytes < (INT64_C(4) << 20) && xcd_merge)
+    return static_cast<int>(std::max<int64_t>(64, (longest / 12 + 63) / 64 * 64));
   if (bytes < (INT64_C(4) << 20)) return static_cast<int>(std::max<int64_t>(64, (longest + 63) / 64 * 64));
   if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 240 + 63) / 64 * 64)));
   return positions >= (INT64_C(1) << 20) ? 1280 : 1024;
@@ -1301,7 +1436,7 @@ static int plan_request(const hexkv_attend_params *p, const int32_t *lens, const
   }
   if (p->partition > 0) return p->partition;
   const int64_t row_bytes = 2 * static_cast<int64_t>(p->head_dim) * elem_size(p->dtype);
-  return plan_chunk(positions, row_bytes, longest);
+  return plan_chunk(positions, row_bytes, longest, p->work_xcds > 0);
 }
 
 }  // namespace hexkv
@@ -1316,6 +1451,105 @@ extern "C" int hexkv_attend_plan_chunk(const hexkv_attend_params *p, const int32
   return HEXKV_OK;
 }
 
+namespace hexkv {
+
+// The work list of a planning request, in launch order (see hexkv_attend_plan),
+// and each (row, head group) segment's partition count.
+static int build_plan(const hexkv_attend_params *p, const int32_t *lens, int64_t chunk,
+                      std::vector<hexkv_work_item> &out, std::vector<int32_t> &seg_parts, int32_t *max_parts,
+                      const char *what) {
+  const int G = kernel_group(p->q_heads / p->kv_heads);
+  const int groups = p->q_heads / G;
+  const int64_t segs = static_cast<int64_t>(p->batch) * groups;
+  const int extra = p->kv_new ? 1 : 0;
+  const int X = std::max(1, p->work_xcds);
+  if (p->work_xcds < 0 || p->work_xcds > 64) return fail(HEXKV_EINVAL, "%s: work_xcds outside [0, 64]", what);
+  if (p->work_xcds > 0 && segs > kCounterWords)
+    return fail(HEXKV_EINVAL, "%s: the single-launch merge counts at most %lld segments", what,
+                static_cast<long long>(kCounterWords));
+  std::vector<int64_t> len(p->batch);
+  int64_t count = 0, most = 1, full_rounds = 0;
+  for (int b = 0; b < p->batch; ++b) {
+    len[b] = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+    const int64_t k = len[b] == 0 ? 1 : (len[b] + chunk - 1) / chunk;
+    count += k * groups;
+    most = std::max(most, k);
+    full_rounds = std::max(full_rounds, len[b] / chunk);
+  }
+  if (most > 65535 || count > INT32_MAX / 2) return fail(HEXKV_EUNSUPPORTED, "%s: more than 65535 partitions per row", what);
+  *max_parts = static_cast<int32_t>(most);
+  seg_parts.assign(static_cast<size_t>(segs), 0);
+  for (int b = 0; b < p->batch; ++b)
+    for (int hg = 0; hg < groups; ++hg)
+      seg_parts[static_cast<size_t>(b) * groups + hg] = static_cast<int32_t>(len[b] == 0 ? 1 : (len[b] + chunk - 1) / chunk);
+
+  // Home XCD of each segment (all on XCD 0 without XCD placement): longest
+  // first, each to the XCD with the fewest positions so far.
+  std::vector<int> home(static_cast<size_t>(segs), 0);
+  if (X > 1) {
+    std::vector<int64_t> order(static_cast<size_t>(segs));
+    for (int64_t i = 0; i < segs; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int64_t x, int64_t y) { return len[x / groups] > len[y / groups]; });
+    std::vector<int64_t> load(X, 0);
+    for (const int64_t sg : order) {
+      const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+      home[sg] = x;
+      load[x] += std::max<int64_t>(len[sg / groups], 1);
+    }
+  }
+  // Each XCD's items: empty rows (a zero output each), then the full chunks,
+  // chunk index by chunk index across its segments, then every segment's
+  // last, shorter chunk from the longest down, so its share ends on its
+  // smallest items.
+  std::vector<std::vector<hexkv_work_item>> lists(X);
+  auto make = [&](int b, int hg, int64_t part, int64_t first, int64_t cnt) {
+    hexkv_work_item it;
+    it.row = b;
+    it.head_group = hg;
+    it.part = static_cast<int32_t>(part);
+    it.parts = seg_parts[static_cast<size_t>(b) * groups + hg];
+    it.first = static_cast<int32_t>(first);
+    it.count = static_cast<int32_t>(cnt);
+    it.len = static_cast<int32_t>(len[b]);
+    it.reserved = 0;
+    lists[home[static_cast<size_t>(b) * groups + hg]].push_back(it);
+  };
+  std::vector<std::pair<int64_t, int64_t>> tails;  // (positions, b * groups + hg)
+  for (int b = 0; b < p->batch; ++b)
+    for (int hg = 0; hg < groups; ++hg) {
+      if (len[b] == 0) make(b, hg, 0, 0, 0);
+      else if (len[b] % chunk) tails.emplace_back(len[b] % chunk, static_cast<int64_t>(b) * groups + hg);
+    }
+  for (int64_t c = 0; c < full_rounds; ++c)
+    for (int b = 0; b < p->batch; ++b) {
+      if ((c + 1) * chunk > len[b]) continue;
+      for (int hg = 0; hg < groups; ++hg) make(b, hg, c, c * chunk, chunk);
+    }
+  std::stable_sort(tails.begin(), tails.end(),
+                   [](const std::pair<int64_t, int64_t> &x, const std::pair<int64_t, int64_t> &y) { return x.first > y.first; });
+  for (const auto &t : tails) {
+    const int b = static_cast<int>(t.second / groups), hg = static_cast<int>(t.second % groups);
+    const int64_t k = (len[b] + chunk - 1) / chunk;
+    make(b, hg, k - 1, (k - 1) * chunk, t.first);
+  }
+  // XCD x's j-th item at index j * X + x; shorter lists padded with items
+  // outside the call's geometry (row = batch), which the kernels skip.
+  size_t longest = 0;
+  for (const auto &l : lists) longest = std::max(longest, l.size());
+  hexkv_work_item pad{};
+  pad.row = p->batch;
+  out.assign(longest * X, pad);
+  for (int x = 0; x < X; ++x)
+    for (size_t j = 0; j < lists[x].size(); ++j) out[j * X + x] = lists[x][j];
+  if (X == 1 && static_cast<int64_t>(out.size()) != count)
+    return fail(HEXKV_EINVAL, "%s: internal count mismatch %zu vs %lld", what, out.size(), static_cast<long long>(count));
+  if (out.size() > static_cast<size_t>(INT32_MAX)) return fail(HEXKV_EUNSUPPORTED, "%s: work list too long", what);
+  return HEXKV_OK;
+}
+
+}  // namespace hexkv
+
 extern "C" int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_work_item *items,
                                  int32_t items_capacity, int32_t *parts, int32_t parts_capacity,
                                  int32_t *n_items, int32_t *max_parts) {
@@ -1325,69 +1559,19 @@ extern "C" int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *le
   if (!n_items || !max_parts) return fail(HEXKV_EINVAL, "%s: null argument", what);
   const int chunk_or_error = plan_request(p, lens, what);
   if (chunk_or_error < 0) return chunk_or_error;
-  const int64_t chunk = chunk_or_error;
-  const int G = kernel_group(p->q_heads / p->kv_heads);
-  const int groups = p->q_heads / G;
-  const int64_t segs = static_cast<int64_t>(p->batch) * groups;
-  const int extra = p->kv_new ? 1 : 0;
-  int64_t count = 0, most = 1, full_rounds = 0;
-  for (int b = 0; b < p->batch; ++b) {
-    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
-    const int64_t k = len == 0 ? 1 : (len + chunk - 1) / chunk;
-    count += k * groups;
-    most = std::max(most, k);
-    full_rounds = std::max(full_rounds, len / chunk);
-  }
-  if (most > 65535 || count > INT32_MAX) return fail(HEXKV_EUNSUPPORTED, "%s: more than 65535 partitions per row", what);
-  *n_items = static_cast<int32_t>(count);
-  *max_parts = static_cast<int32_t>(most);
+  std::vector<hexkv_work_item> list;
+  std::vector<int32_t> seg_parts;
+  int32_t most = 1;
+  const int rc = build_plan(p, lens, chunk_or_error, list, seg_parts, &most, what);
+  if (rc != HEXKV_OK) return rc;
+  *n_items = static_cast<int32_t>(list.size());
+  *max_parts = most;
   if (!items) return HEXKV_OK;  // a size query
-  if (items_capacity < count || !parts || parts_capacity < segs)
-    return fail(HEXKV_EINVAL, "%s: room for %d items and %d segment counts given, %lld and %lld needed", what,
-                items_capacity, parts_capacity, static_cast<long long>(count), static_cast<long long>(segs));
-  // Order: empty rows (a zero output each), then the full chunks, chunk index
-  // by chunk index across all (row, head group) segments, then every row's
-  // last, shorter chunk from the longest down, so the launch ends on its
-  // smallest items.
-  int64_t n = 0;
-  auto put = [&](int b, int hg, int64_t part, int64_t k, int64_t first, int64_t cnt, int64_t len) {
-    hexkv_work_item &it = items[n++];
-    it.row = b;
-    it.head_group = hg;
-    it.part = static_cast<int32_t>(part);
-    it.parts = static_cast<int32_t>(k);
-    it.first = static_cast<int32_t>(first);
-    it.count = static_cast<int32_t>(cnt);
-    it.len = static_cast<int32_t>(len);
-    it.reserved = 0;
-  };
-  std::vector<std::pair<int64_t, int64_t>> tails;  // (positions, b * groups + hg)
-  for (int b = 0; b < p->batch; ++b) {
-    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
-    const int64_t k = len == 0 ? 1 : (len + chunk - 1) / chunk;
-    for (int hg = 0; hg < groups; ++hg) {
-      parts[static_cast<int64_t>(b) * groups + hg] = static_cast<int32_t>(k);
-      if (len == 0) put(b, hg, 0, 1, 0, 0, 0);
-      else if (len % chunk) tails.emplace_back(len % chunk, static_cast<int64_t>(b) * groups + hg);
-    }
-  }
-  for (int64_t c = 0; c < full_rounds; ++c)
-    for (int b = 0; b < p->batch; ++b) {
-      const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
-      if ((c + 1) * chunk > len) continue;
-      const int64_t k = (len + chunk - 1) / chunk;
-      for (int hg = 0; hg < groups; ++hg) put(b, hg, c, k, c * chunk, chunk, len);
-    }
-  std::stable_sort(tails.begin(), tails.end(),
-                   [](const std::pair<int64_t, int64_t> &x, const std::pair<int64_t, int64_t> &y) { return x.first > y.first; });
-  for (const auto &t : tails) {
-    const int b = static_cast<int>(t.second / groups), hg = static_cast<int>(t.second % groups);
-    const int64_t len = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
-    const int64_t k = (len + chunk - 1) / chunk;
-    put(b, hg, k - 1, k, (k - 1) * chunk, t.first, len);
-  }
-  if (n != count) return fail(HEXKV_EINVAL, "%s: internal count mismatch %lld vs %lld", what,
-                              static_cast<long long>(n), static_cast<long long>(count));
+  if (items_capacity < static_cast<int64_t>(list.size()) || !parts || parts_capacity < static_cast<int64_t>(seg_parts.size()))
+    return fail(HEXKV_EINVAL, "%s: room for %d items and %d segment counts given, %zu and %zu needed", what,
+                items_capacity, parts_capacity, list.size(), seg_parts.size());
+  std::copy(list.begin(), list.end(), items);
+  std::copy(seg_parts.begin(), seg_parts.end(), parts);
   return HEXKV_OK;
 }
 
@@ -1454,13 +1638,24 @@ static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t w
   a.ws_o = nullptr;
   a.ws_ml = nullptr;
   if (need > 0) {
-    a.ws_o = static_cast<float *>(workspace);
+    a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + HEXKV_ATTEND_COUNTER_BYTES);
     a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
   }
   a.n_groups = p->q_heads / G;
   a.rows = static_cast<int32_t>(rows);
   a.items = p->work_items_dev;
   a.seg_parts = p->work_parts_dev;
+  // Split segments of a list planned for the XCDs merge in the attention
+  // kernel, counting arrivals in the workspace's counter words.
+  a.seg_count = (a.items && p->work_xcds > 0 && p->work_xcds <= 8 && need > 0 && max_parts <= kMergeMaxParts &&
+                 G * p->head_dim <= 4 * kAttThreads)
+                    ? static_cast<uint64_t *>(workspace) : nullptr;
+  a.n_xcd = p->work_xcds;
+  a.lengths_out = p->lengths_out_dev;
+  // The status word, where a kernel may raise a flag: lengths read from
+  // seqlens (clamped), XCD placement of a single-launch merge.
+  if (((a.seqlens && !a.items) || a.seg_count) && (rc = status_word(stream, &a.status, what)) != HEXKV_OK)
+    return rc;
 
   dim3 grid;
   if (a.items) {
@@ -1488,45 +1683,17 @@ static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t w
 // hexkv_attend_noalloc's workspace: one array per GPU the library runs on,
 // held until the process ends.  Host code never passes `scratch` itself to a
 // kernel (in host code the name is a stand-in, not a device address); it
-// uses the per-device address hipGetSymbolAddress returns.
+// uses the per-device address hipGetSymbolAddress returns.  Like every
+// file-scope variable it starts zero, so its arrival counters (the first
+// HEXKV_ATTEND_COUNTER_BYTES, which every call leaves zero) need no clearing.
 static __device__ __align__(256) unsigned char scratch[HEXKV_NOALLOC_SCRATCH_BYTES];
-
-constexpr int kMaxScratchDevices = 64;
-static std::atomic<void *> g_scratch_addr[kMaxScratchDevices];
-static std::mutex g_scratch_mu;
+static std::atomic<void *> g_scratch_addr[kMaxDevices];
 
 // Device address of `scratch` on the device that runs `stream` (the current
 // device for the null stream), looked up once per device with that device
 // current.
 static int scratch_address(hexkv_stream_t stream, void **addr, const char *what) {
-  int dev = 0;
-  hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev) : hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: cannot tell the stream's device: %s", what, hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxScratchDevices)
-    return fail(HEXKV_EUNSUPPORTED, "%s: device %d beyond the %d the library tracks", what, dev, kMaxScratchDevices);
-  void *ptr = g_scratch_addr[dev].load(std::memory_order_acquire);
-  if (ptr) {
-    *addr = ptr;
-    return HEXKV_OK;
-  }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  ptr = g_scratch_addr[dev].load(std::memory_order_relaxed);
-  if (!ptr) {
-    int current = 0;
-    e = hipGetDevice(&current);
-    if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
-    if (current != dev && (e = hipSetDevice(dev)) != hipSuccess)
-      return fail(HEXKV_EHIP, "%s: hipSetDevice(%d): %s", what, dev, hipGetErrorString(e));
-    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    const hipError_t back = current != dev ? hipSetDevice(current) : hipSuccess;
-    if (e != hipSuccess || !ptr)
-      return fail(HEXKV_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev, hipGetErrorString(e));
-    if (back != hipSuccess)
-      return fail(HEXKV_EHIP, "%s: restoring device %d: %s", what, current, hipGetErrorString(back));
-    g_scratch_addr[dev].store(ptr, std::memory_order_release);
-  }
-  *addr = ptr;
-  return HEXKV_OK;
+  return symbol_address(reinterpret_cast<const void *>(&HIP_SYMBOL(scratch)), g_scratch_addr, stream, addr, what);
 }
 
 }  // namespace hexkv
@@ -1664,7 +1831,7 @@ extern "C" int hexkv_ft_attend(const hexkv_ft_attend_params *p, void *workspace,
   a.capacity = cap;
   a.scale_log2 = p->softmax_scale * 1.4426950408889634f;
   if (need > 0) {
-    a.ws_o = static_cast<float *>(workspace);
+    a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + HEXKV_ATTEND_COUNTER_BYTES);
     a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
   }
   a.rows = static_cast<int32_t>(rows);
@@ -1679,6 +1846,7 @@ extern "C" int hexkv_ft_attend(const hexkv_ft_attend_params *p, void *workspace,
   a.rot_dim = p->rotary_dim;
   a.rot_neox = p->rotary_neox ? 1 : 0;
   a.rot_log2_base = p->rotary_dim > 0 ? log2(static_cast<double>(p->rotary_base)) : 0.0;
+  if (p->positions_dev && (rc = status_word(stream, &a.status, "hexkv_ft_attend")) != HEXKV_OK) return rc;
 
   const unsigned grid_x = static_cast<unsigned>(max_parts | 1);  // odd: see hexkv_attend
   dim3 grid(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));

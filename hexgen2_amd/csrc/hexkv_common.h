@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "hexkv.h"
 
 namespace hexkv {
@@ -17,6 +19,23 @@ void clear_error();
 
 // Turns a pending launch error into HEXKV_EHIP.
 int check_launch(const char *what);
+
+// Devices whose per-device addresses the library caches.
+constexpr int kMaxDevices = 64;
+
+// The device `stream` runs on (the current device for the null stream).
+int stream_device(hexkv_stream_t stream, int *dev, const char *what);
+
+// Device address of a file-scope __device__ variable on the device that runs
+// `stream`, looked up once per device (with that device current) and kept
+// in cache[device].  `symbol` is the variable's host-side name, which is not
+// a device address itself.
+int symbol_address(const void *symbol, std::atomic<void *> *cache, hexkv_stream_t stream, void **addr,
+                   const char *what);
+
+// Device address of the status word (HEXKV_STATUS_* bits) of the device that
+// runs `stream`.
+int status_word(hexkv_stream_t stream, unsigned int **word, const char *what);
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -31,7 +50,34 @@ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 __device__ __forceinline__ bf16x2 as_bf16x2(unsigned int w) { return __builtin_bit_cast(bf16x2, w); }
 __device__ __forceinline__ f16x2 as_f16x2(unsigned int w) { return __builtin_bit_cast(f16x2, w); }
 
+// Whether a work item read from device memory lies inside a call's
+// geometry: row, head group and partition in range, positions
+// [first, first + count) within the row's length, the length within
+// max_seqlen.  Written without sums that could overflow (first and count are
+// checked non-negative first), so an item with extreme values is rejected
+// rather than wrapped into range.  Items outside do nothing.
+__host__ __device__ inline bool work_item_fits(const hexkv_work_item &it, int rows, int n_groups, int max_parts,
+                                               int max_seqlen) {
+  return static_cast<unsigned>(it.row) < static_cast<unsigned>(rows) &&
+         static_cast<unsigned>(it.head_group) < static_cast<unsigned>(n_groups) &&
+         static_cast<unsigned>(it.part) < static_cast<unsigned>(max_parts) && it.parts >= 1 &&
+         it.parts <= max_parts && it.first >= 0 && it.count >= 0 && it.len <= max_seqlen &&
+         it.count <= it.len - it.first;
+}
+
 // ---------------------------------------------------------------- device ---
+
+// Raises status flags (a device-scope atomic OR; `word` may be null).
+__device__ __forceinline__ void raise_status(unsigned int *word, unsigned int flags) {
+  if (word) atomicOr(word, flags);
+}
+
+// The XCD (die) this wave runs on.
+__device__ __forceinline__ int xcd_id() {
+  int x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x & 0xf;
+}
 
 // Cross-lane reductions, all VALU data movement (no LDS round trip):
 // partners within a 16-lane row move by DPP (quad permutes, half-row and row

@@ -116,10 +116,14 @@ __global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const A a) {
 template <typename V>
 __global__ __launch_bounds__(kAppendThreads) void append_kernel(
     const char *__restrict__ kv_new, char *__restrict__ cache, int64_t seq_stride_bytes,
-    int64_t capacity, int64_t row_bytes, const int32_t *__restrict__ positions, int32_t bias) {
+    int64_t capacity, int64_t row_bytes, const int32_t *__restrict__ positions, int32_t bias,
+    unsigned int *status) {
   const int b = blockIdx.y;
   const int64_t pos = (positions ? static_cast<int64_t>(positions[b]) : 0) + bias;
-  if (pos < 0 || pos >= capacity) return;
+  if (pos < 0 || pos >= capacity) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) raise_status(status, HEXKV_STATUS_APPEND_SKIPPED);
+    return;
+  }
   const int64_t nv = row_bytes / static_cast<int64_t>(sizeof(V));
   const V *s = reinterpret_cast<const V *>(kv_new + b * row_bytes);
   V *d = reinterpret_cast<V *>(cache + b * seq_stride_bytes + pos * row_bytes);
@@ -270,11 +274,18 @@ extern "C" int hexkv_append(const void *kv_new, void *cache, int batch, int64_t 
   dim3 grid(gx, static_cast<unsigned>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t stride = seq_stride_rows * row_bytes;
+  // Positions read on the device can fall outside the cache: such rows are
+  // skipped and reported through the status word.
+  unsigned int *status = nullptr;
+  if (positions_dev) {
+    const int rc = status_word(stream, &status, "hexkv_append");
+    if (rc != HEXKV_OK) return rc;
+  }
   if (vec16)
     append_kernel<u32x4><<<grid, kAppendThreads, 0, s>>>(static_cast<const char *>(kv_new),
-        static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias);
+        static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias, status);
   else
     append_kernel<unsigned int><<<grid, kAppendThreads, 0, s>>>(static_cast<const char *>(kv_new),
-        static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias);
+        static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias, status);
   return check_launch("hexkv_append");
 }

@@ -1,6 +1,9 @@
-// Per-thread error reporting and version of the hexkv C ABI.
+// Per-thread error reporting, version, the per-GPU device status word and the
+// device queries of the hexkv C ABI.
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <mutex>
 
 #include "hexkv_common.h"
 
@@ -24,8 +27,91 @@ int check_launch(const char *what) {
   return HEXKV_OK;
 }
 
+int stream_device(hexkv_stream_t stream, int *dev, const char *what) {
+  const hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), dev) : hipGetDevice(dev);
+  if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: cannot tell the stream's device: %s", what, hipGetErrorString(e));
+  if (*dev < 0 || *dev >= kMaxDevices)
+    return fail(HEXKV_EUNSUPPORTED, "%s: device %d beyond the %d the library tracks", what, *dev, kMaxDevices);
+  return HEXKV_OK;
+}
+
+static std::mutex g_symbol_mu;
+
+int symbol_address(const void *symbol, std::atomic<void *> *cache, hexkv_stream_t stream, void **addr,
+                   const char *what) {
+  int dev = 0;
+  int rc = stream_device(stream, &dev, what);
+  if (rc != HEXKV_OK) return rc;
+  void *ptr = cache[dev].load(std::memory_order_acquire);
+  if (ptr) {
+    *addr = ptr;
+    return HEXKV_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_symbol_mu);
+  ptr = cache[dev].load(std::memory_order_relaxed);
+  if (!ptr) {
+    int current = 0;
+    hipError_t e = hipGetDevice(&current);
+    if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+    if (current != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(HEXKV_EHIP, "%s: hipSetDevice(%d): %s", what, dev, hipGetErrorString(e));
+    e = hipGetSymbolAddress(&ptr, symbol);
+    const hipError_t back = current != dev ? hipSetDevice(current) : hipSuccess;
+    if (e != hipSuccess || !ptr)
+      return fail(HEXKV_EHIP, "%s: hipGetSymbolAddress on device %d: %s", what, dev, hipGetErrorString(e));
+    if (back != hipSuccess)
+      return fail(HEXKV_EHIP, "%s: restoring device %d: %s", what, current, hipGetErrorString(back));
+    cache[dev].store(ptr, std::memory_order_release);
+  }
+  *addr = ptr;
+  return HEXKV_OK;
+}
+
+// The status word of each GPU (HEXKV_STATUS_* bits, raised by kernels with
+// atomicOr).  Host code passes kernels the per-device address that
+// hipGetSymbolAddress returns, never the name itself.
+static __device__ unsigned int device_status;
+static std::atomic<void *> g_status_addr[kMaxDevices];
+
+int status_word(hexkv_stream_t stream, unsigned int **word, const char *what) {
+  void *ptr = nullptr;
+  const int rc = symbol_address(reinterpret_cast<const void *>(&HIP_SYMBOL(device_status)), g_status_addr, stream,
+                                &ptr, what);
+  *word = static_cast<unsigned int *>(ptr);
+  return rc;
+}
+
 }  // namespace hexkv
 
-extern "C" int hexkv_version(void) { return 100; /* 0.1.0 */ }
+extern "C" int hexkv_version(void) { return 200; /* 0.2.0 */ }
 
 extern "C" const char *hexkv_last_error(void) { return hexkv::g_last_error; }
+
+extern "C" int hexkv_device_status(uint32_t *flags, int clear, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_device_status";
+  if (!flags) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  unsigned int *word = nullptr;
+  int rc = status_word(stream, &word, what);
+  if (rc != HEXKV_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipStreamSynchronize(s);
+  if (e == hipSuccess) e = hipMemcpyAsync(flags, word, sizeof(*flags), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && clear) e = hipMemsetAsync(word, 0, sizeof(*word), s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return HEXKV_OK;
+}
+
+extern "C" int hexkv_device_xcds(int32_t *xcds) {
+  using namespace hexkv;
+  clear_error();
+  if (!xcds) return fail(HEXKV_EINVAL, "hexkv_device_xcds: null argument");
+  int dev = 0, n = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev);
+  if (e != hipSuccess) return fail(HEXKV_EHIP, "hexkv_device_xcds: %s", hipGetErrorString(e));
+  *xcds = n > 0 ? n : 1;
+  return HEXKV_OK;
+}

@@ -25,6 +25,7 @@ import torch
 from . import ops
 from .generation import CacheState
 from .llama import LlamaHost, LlamaShape, read_config
+from .mha import check_kv_status
 
 
 # Packed handoff buffers at or above this size are allocated per layer, so
@@ -111,6 +112,7 @@ class Engine:
         ops.unpack_live(live, full, [prompt_length])
         for i in range(n_layers):
             state.key_value_memory_dict[i] = full[i]
+        ops.device_status(self.device)  # report only what this decode's kernels meet
         for _ in range(max_new_tokens - 1):
             logits = self.model.forward(token[:, None], inference_params=state, last_token_only=True,
                                         fused_append=self.fused_append)
@@ -119,6 +121,9 @@ class Engine:
                 on_logits(logits)
             token = logits.argmax(-1)
             generated.append(int(token.item()))
+            # the token read synchronised: report any out-of-contract device
+            # position the step's kernels met (mha.py:281-282's assert)
+            check_kv_status(self.device)
             if on_token:
                 on_token(generated[-1])
         return generated

@@ -3,9 +3,11 @@
 * ``_update_kv_cache(kv, inference_params, layer_idx)`` -- append (and the
   prefill write) into the per-layer cache; hexgen/hexgen_core/modules/
   mha.py:255-288.
-* ``allocate_inference_cache(...)`` -- ``MHA.allocate_inference_cache``
-  (mha.py:414-428): the ``[B, S, 2, H, D]`` cache, or with
-  ``fused_ft_kernel=True`` the FasterTransformer (FT) K/V pair.
+* ``inference_cache(...)`` -- one layer's cache in the shapes of
+  ``MHA.allocate_inference_cache`` (mha.py:414-428): the ``[B, S, 2, H, D]``
+  cache, or with ``fused_ft_kernel=True`` the FasterTransformer (FT) K/V pair.
+* ``check_kv_status()`` -- the device-side capacity check of ragged appends
+  (mha.py:281-282), reported at the caller's next synchronisation.
 * ``_apply_rotary_single_query_attention(...)`` -- the FT decode step
   (mha.py:310-337): rotary, append and attention over the FT caches.
 * ``FlashCrossAttention`` -- the attention module the reference's MHA calls at
@@ -24,12 +26,16 @@ from torch import nn
 from . import ops
 
 
-def allocate_inference_cache(batch_size: int, max_seqlen: int, num_heads_kv: int, head_dim: int,
-                             dtype: torch.dtype, device, fused_ft_kernel: bool = False):
-    """``torch.empty(batch, max_seqlen, 2, kv_heads, head_dim)`` (mha.py:418-420),
-    or with ``fused_ft_kernel`` the FT pair ``(K [batch, kv_heads, head_dim /
-    pack, max_seqlen, pack], V [batch, kv_heads, max_seqlen, head_dim])``,
-    pack = 4 for float32 and 8 for 16-bit data (mha.py:421-428)."""
+def inference_cache(batch_size: int, max_seqlen: int, num_heads_kv: int, head_dim: int,
+                    dtype: torch.dtype, device, fused_ft_kernel: bool = False):
+    """One layer's cache in the shapes ``MHA.allocate_inference_cache``
+    gives it: ``torch.empty(batch, max_seqlen, 2, kv_heads, head_dim)``
+    (mha.py:418-420), or with ``fused_ft_kernel`` the FT pair ``(K [batch,
+    kv_heads, head_dim / pack, max_seqlen, pack], V [batch, kv_heads,
+    max_seqlen, head_dim])``, pack = 4 for float32 and 8 for 16-bit data
+    (mha.py:421-428).  The head geometry, dtype and device are arguments here
+    (the reference method reads them from the module); the reference method
+    itself needs no replacement, since it only calls ``torch.empty``."""
     if not fused_ft_kernel:
         return torch.empty(batch_size, max_seqlen, 2, num_heads_kv, head_dim, dtype=dtype, device=device)
     assert dtype in (torch.float16, torch.bfloat16, torch.float32)
@@ -48,9 +54,11 @@ def _sample_positions(inference_params, batch_start: int, batch_end: int) -> Opt
     token is written at), or None when the batch shares
     ``sequence_len_offset``.  ``lengths_per_sample`` is the field the
     reference reads per-sample positions from (generation.py:30, used at
-    mha.py:327-328)."""
+    mha.py:327-328), and only for decode steps: at ``sequence_len_offset``
+    0 (the prompt, where the reference's generation loop has already set it
+    to the prompt lengths, generation.py:380) the write goes to the offset."""
     lengths = inference_params.lengths_per_sample
-    if lengths is None:
+    if lengths is None or inference_params.sequence_len_offset == 0:
         return None
     if lengths.dim() != 1 or lengths.shape[0] < batch_end:
         raise ValueError(f"lengths_per_sample of shape {tuple(lengths.shape)} does not cover "
@@ -75,15 +83,18 @@ def _update_kv_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torc
     position (the returned view spans ``sequence_len_offset + 1`` positions),
     and the view carries the per-sample key counts so that
     ``FlashCrossAttention`` attends ``lengths_per_sample[b] + 1`` keys of
-    row b rather than the whole view."""
+    row b rather than the whole view.  The positions live in device memory,
+    so the reference's capacity assert (mha.py:281-282) becomes a device
+    check: a position past the cache is not written, a row past the view is
+    cut to it, and ``check_kv_status`` raises ValueError for either at the
+    caller's next synchronisation."""
     if inference_params.fused_ft_kernel:
         return _update_ft_cache(kv, inference_params, layer_idx)
     num_heads, head_dim = kv.shape[-2:]
     cache = inference_params.key_value_memory_dict.get(layer_idx)
     if cache is None:
-        cache = allocate_inference_cache(inference_params.max_batch_size,
-                                         inference_params.max_sequence_len, num_heads, head_dim,
-                                         kv.dtype, kv.device)
+        cache = inference_cache(inference_params.max_batch_size, inference_params.max_sequence_len,
+                                num_heads, head_dim, kv.dtype, kv.device)
         inference_params.key_value_memory_dict[layer_idx] = cache
     batch_start = inference_params.batch_size_offset
     batch_end = batch_start + kv.shape[0]
@@ -120,8 +131,8 @@ def _update_ft_cache(kv: torch.Tensor, inference_params, layer_idx: int) -> torc
     num_heads, head_dim = kv.shape[-2:]
     caches = inference_params.key_value_memory_dict.get(layer_idx)
     if caches is None:
-        caches = allocate_inference_cache(inference_params.max_batch_size, inference_params.max_sequence_len,
-                                          num_heads, head_dim, kv.dtype, kv.device, fused_ft_kernel=True)
+        caches = inference_cache(inference_params.max_batch_size, inference_params.max_sequence_len,
+                                 num_heads, head_dim, kv.dtype, kv.device, fused_ft_kernel=True)
         inference_params.key_value_memory_dict[layer_idx] = caches
     k_cache, v_cache = caches
     batch_start = inference_params.batch_size_offset
@@ -219,6 +230,15 @@ class FlashCrossAttention(nn.Module):
                                     softmax_scale=self.softmax_scale)
 
 
+def check_kv_status(device=None) -> None:
+    """Raise ValueError if a cache append or attention since the last check
+    met a per-sample position (``lengths_per_sample``) outside the cache or
+    the attended view: the device-side form of the reference's capacity
+    assert (mha.py:281-282).  It synchronises the current stream; decode
+    loops call it where they read the token anyway."""
+    ops.check_device_status(device)
+
+
 def update_and_attend(q: torch.Tensor, kv: torch.Tensor, inference_params, layer_idx: int,
                       softmax_scale: Optional[float] = None) -> torch.Tensor:
     """The decode-step pair ``_update_kv_cache`` + ``inner_cross_attn(q, kv,
@@ -226,7 +246,8 @@ def update_and_attend(q: torch.Tensor, kv: torch.Tensor, inference_params, layer
     written to the cache and attended from registers.  q (B, 1, H, D),
     kv (B, 1, 2, H_k, D).  With ``lengths_per_sample`` set, row b is written
     at ``lengths_per_sample[b]`` and attends that many keys plus the new one;
-    ``sequence_len_offset`` bounds every sample's position."""
+    ``sequence_len_offset`` bounds every sample's position (checked on the
+    device, reported by ``check_kv_status``)."""
     cache = inference_params.key_value_memory_dict[layer_idx]
     batch_start = inference_params.batch_size_offset
     batch_end = batch_start + kv.shape[0]

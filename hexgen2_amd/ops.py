@@ -45,6 +45,53 @@ def _stream(t) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+@functools.lru_cache(maxsize=None)
+def device_xcds(index: int) -> int:
+    """XCDs (dies with their own L2) of HIP device ``index``
+    (``hexkv_device_xcds``): what a work list is planned for when its split
+    segments merge inside the attention kernel."""
+    n = ctypes.c_int32()
+    with torch.cuda.device(index):
+        _lib.check(_lib.load().hexkv_device_xcds(ctypes.byref(n)), "hexkv_device_xcds")
+    return n.value
+
+
+_STATUS_TEXT = {
+    _lib.STATUS_APPEND_SKIPPED: "an append position read from device memory fell outside the cache, "
+                                "so that row was not written",
+    _lib.STATUS_LENGTH_CLAMPED: "a sequence length read from device memory exceeded the attended view "
+                                "(max_seqlen) and was cut to it, so that row missed keys (with a fused "
+                                "append, its own new key)",
+    _lib.STATUS_PLACEMENT: "the work items of a split segment ran on more than one XCD, so that segment's "
+                           "single-launch merge may have read stale partials",
+}
+
+
+def device_status(device=None, clear: bool = True) -> int:
+    """The HEXKV_STATUS_* flags the kernels raised on ``device`` (default:
+    the current one) since the last clear, after the current stream's work
+    has finished; resets them when ``clear``."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    flags = ctypes.c_uint32()
+    with torch.cuda.device(dev):
+        rc = _lib.load().hexkv_device_status(ctypes.byref(flags), 1 if clear else 0,
+                                             ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    _lib.check(rc, "hexkv_device_status")
+    return flags.value
+
+
+def check_device_status(device=None) -> None:
+    """Raise ValueError if a kernel met out-of-contract values in device
+    memory since the last check (clearing the flags): the device-side
+    counterpart of the reference's capacity assert (hexgen/hexgen_core/
+    modules/mha.py:281-282).  It synchronises, so callers run it where they
+    synchronise anyway (after reading a token)."""
+    flags = device_status(device, clear=True) & _lib.STATUS_ERRORS
+    if flags:
+        text = "; ".join(t for bit, t in _STATUS_TEXT.items() if flags & bit)
+        raise ValueError(f"hexkv device status {flags:#x}: {text}")
+
+
 def _contiguous(shape, stride) -> bool:
     """``Tensor.is_contiguous()`` of a view with these sizes and strides,
     without building the view (size-1 dims are free; an empty view is
@@ -316,7 +363,8 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
                      kv_new: Optional[torch.Tensor] = None, causal: bool = False,
                      softmax_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
                      workspace: Optional[torch.Tensor] = None, partition: int = 0,
-                     kernel: str = "auto", lens: Optional[Sequence[int]] = None) -> torch.Tensor:
+                     kernel: str = "auto", lens: Optional[Sequence[int]] = None,
+                     single_launch: bool = True) -> torch.Tensor:
     """Attention of ``q [B, q_len, Hq, D]`` over a cache ``[B, S, 2, Hkv, D]``.
 
     Sequence b attends to ``len_b = seqlens[b] + seqlen_bias`` keys (the
@@ -329,7 +377,11 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     (packed dot products), "mfma" (the GQA group on the matrix cores, 16-bit
     only) or "auto" (the library's choice).  ``lens``, the host values of
     ``seqlens`` (decode rows), makes the call run a work list
-    (``hexkv_attend_plan``; ``partition`` then sets its chunk size).
+    (``hexkv_attend_plan``; ``partition`` then sets its chunk size).  With
+    ``single_launch`` the list is planned for the device's XCDs and split rows
+    merge inside the attention kernel (one launch); otherwise a second kernel
+    merges them.  A caller-supplied ``workspace`` must have been zeroed once
+    after allocation (its leading counter words; every call leaves them zero).
     """
     _require_device(q, cache)
     if out is None:
@@ -339,13 +391,13 @@ def decode_attention(q: torch.Tensor, cache: torch.Tensor, *, max_seqlen: int,
     lib = _lib.load()
     work = None
     if lens is not None:
-        work = _plan_work(p, lens, q.device)  # kept alive until the launch is enqueued
+        work = _plan_work(p, lens, q.device, single_launch)  # kept alive until the launch is enqueued
         work.apply(p)
     need = int(lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
     ws_ptr, ws_bytes = None, 0
     if need:
         if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+            workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
         _require_device(workspace)
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     rc = lib.hexkv_attend(ctypes.byref(p), ws_ptr, ws_bytes, _stream(q))
@@ -359,20 +411,49 @@ class WorkList:
     ``parts`` (partitions per (row, head group)), valid for the lengths and
     ``seqlen_bias``/``max_seqlen`` it was built for."""
 
-    def __init__(self, items: torch.Tensor, parts: torch.Tensor, n_items: int, max_parts: int):
+    def __init__(self, items: torch.Tensor, parts: torch.Tensor, n_items: int, max_parts: int, xcds: int = 0):
         self.items, self.parts, self.n_items, self.max_parts = items, parts, n_items, max_parts
+        self.xcds = xcds
 
     def apply(self, p: _lib.AttendParams) -> None:
         p.work_items_dev, p.work_parts_dev = self.items.data_ptr(), self.parts.data_ptr()
-        p.n_work_items, p.work_max_parts = self.n_items, self.max_parts
+        p.n_work_items, p.work_max_parts, p.work_xcds = self.n_items, self.max_parts, self.xcds
 
 
-def _plan_work(p: _lib.AttendParams, lens: Sequence[int], device) -> WorkList:
+def _kernel_group(group: int) -> int:
+    """Query heads per workgroup for a GQA group (the library's rule)."""
+    for g in (8, 4, 2, 1):
+        if group % g == 0:
+            return g
+    return 1
+
+
+def _plan_xcds(p: _lib.AttendParams, device, single_launch: bool) -> int:
+    """work_xcds for a list of these parameters: the device's XCD count when
+    split segments are to merge in the attention kernel (and the counters
+    cover every segment), else 0."""
+    if not single_launch:
+        return 0
+    groups = p.q_heads // _kernel_group(p.q_heads // p.kv_heads)
+    if p.batch * groups > _lib.ATTEND_COUNTER_WORDS:
+        return 0
+    xcds = device_xcds(torch.device(device).index or 0)
+    return xcds if 1 < xcds <= 8 else 0
+
+
+def _plan_work(p: _lib.AttendParams, lens: Sequence[int], device, single_launch: bool = True) -> WorkList:
     """Build the work list on the host (``hexkv_attend_plan``) and copy it to
-    ``device`` on the current stream (asynchronously, from pinned memory)."""
+    ``device`` on the current stream (asynchronously, from pinned memory).
+    Refused under graph capture: the capture would record a copy from a
+    temporary host buffer, replayed later with whatever it then holds (a
+    captured decode step takes its lists from ``StepWorkLists``)."""
+    if torch.cuda.is_current_stream_capturing():
+        raise ValueError("work lists cannot be planned under graph capture: build them before capture "
+                         "(StepWorkLists, AttendPlan.fix_work_list, DecodeStepGraph(lens=...))")
     lib = _lib.load()
     if len(lens) != p.batch:
         raise ValueError(f"{len(lens)} host lengths for a batch of {p.batch}")
+    p.work_xcds = _plan_xcds(p, device, single_launch)
     c_lens = (ctypes.c_int32 * len(lens))(*[int(n) for n in lens])
     n_items, max_parts = ctypes.c_int32(), ctypes.c_int32()
     _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n_items),
@@ -384,7 +465,7 @@ def _plan_work(p: _lib.AttendParams, lens: Sequence[int], device) -> WorkList:
                                      ctypes.c_void_p(parts.data_ptr()), parts.shape[0], ctypes.byref(n_items),
                                      ctypes.byref(max_parts)), "hexkv_attend_plan")
     return WorkList(items.to(device, non_blocking=True), parts.to(device, non_blocking=True),
-                    n_items.value, max_parts.value)
+                    n_items.value, max_parts.value, p.work_xcds)
 
 
 def decode_attention_noalloc(q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *, max_seqlen: int,
@@ -563,19 +644,21 @@ class AttendPlan:
 
     Building the parameter block once and patching only pointers, the length
     bias and ``max_seqlen`` per call keeps host overhead per layer small; the
-    workspace is allocated once for the largest ``max_seqlen`` the loop will
-    use.  Every call checks that q, cache, out and kv_new have exactly the
-    geometry (shape, strides, dtype, device) the block was built for, since
-    only their addresses are patched.  Each call launches on the current
-    stream (so a call inside ``torch.cuda.graph`` capture is recorded into
-    the graph).  Arguments as for ``decode_attention``; a plan built with
-    ``kv_new`` is called with one.
+    workspace is allocated (zeroed) once for the largest ``max_seqlen`` the
+    loop will use.  Every call checks that q, cache, out and kv_new have
+    exactly the geometry (shape, strides, dtype, device) the block was built
+    for, since only their addresses are patched.  Each call launches on the
+    current stream, so a call inside graph capture is recorded into the graph
+    -- with a work list fixed beforehand (``fix_work_list``): planning one
+    under capture is refused.  Arguments as for ``decode_attention``; a plan
+    built with ``kv_new`` is called with one.
     """
 
     def __init__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *,
                  max_seqlens: Sequence[int], seqlens: Optional[torch.Tensor] = None,
                  kv_new: Optional[torch.Tensor] = None, softmax_scale: Optional[float] = None,
-                 partition: int = 0, kernel: str = "auto", lens: Optional[Sequence[int]] = None):
+                 partition: int = 0, kernel: str = "auto", lens: Optional[Sequence[int]] = None,
+                 single_launch: bool = True):
         """``lens``: the host values of ``seqlens`` (decode rows).  With them
         each call runs a work list (``hexkv_attend_plan``: compact, largest
         items first) built once per (``seqlen_bias``, ``max_seqlen``) and
@@ -590,13 +673,20 @@ class AttendPlan:
             for m in max_seqlens:
                 self.params.max_seqlen = int(m)
                 need = max(need, int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params))))
-        self.workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+        self.workspace = torch.zeros(max(need, 16), dtype=torch.uint8, device=q.device)
         self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), self.workspace.numel()
         self.device = q.device
         self.fused = kv_new is not None
+        self.single_launch = single_launch
         self.geometry = _plan_geometry(q, cache, out, kv_new)
         self.lens = None if lens is None else [int(n) for n in lens]
         self.work_key, self.work = None, None
+
+    def _grow_workspace(self) -> None:
+        need = int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params)))
+        if need > self.ws_bytes:
+            self.workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
+            self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), need
 
     def _use_work_list(self, seqlen_bias: int, max_seqlen: int) -> None:
         """Point the parameter block at the work list for this step (built
@@ -605,26 +695,29 @@ class AttendPlan:
         key = (int(seqlen_bias), int(max_seqlen))
         if key != self.work_key:
             p.work_items_dev = None
-            self.work = _plan_work(p, self.lens, self.device)
+            self.work = _plan_work(p, self.lens, self.device, self.single_launch)
             self.work_key = key
         self.work.apply(p)
-        need = int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
-        if need > self.ws_bytes:
-            self.workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
-            self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), need
+        self._grow_workspace()
 
     def fix_work_list(self, work: WorkList) -> None:
-        """Run every later call on ``work``, whose device buffers the caller
-        refills in place between calls (a captured graph's replays): the
-        per-call list building stops, and the workspace grows to fit
-        ``work.max_parts``."""
+        """Run every later call on ``work`` (until the next ``fix_work_list``):
+        the per-call list building stops, and the workspace grows to fit the
+        list.  A workspace a captured graph holds must already fit: size it
+        first with ``reserve``."""
         p = self.params
         self.lens, self.work_key, self.work = None, None, work
         work.apply(p)
-        need = int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
-        if need > self.ws_bytes:
-            self.workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
-            self.ws_ptr, self.ws_bytes = self.workspace.data_ptr(), need
+        self._grow_workspace()
+
+    def reserve(self, lists: Sequence[WorkList]) -> None:
+        """Grow the workspace once to fit every list in ``lists``."""
+        p = self.params
+        saved = (p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds)
+        for work in lists:
+            work.apply(p)
+            self._grow_workspace()
+        (p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds) = saved
 
     def check(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
               kv_new: Optional[torch.Tensor]) -> None:
@@ -632,7 +725,10 @@ class AttendPlan:
         _check_plan_geometry(self.geometry, _plan_geometry(q, cache, out, kv_new))
 
     def __call__(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
-                 kv_new: Optional[torch.Tensor], seqlen_bias: int, max_seqlen: int) -> torch.Tensor:
+                 kv_new: Optional[torch.Tensor], seqlen_bias: int, max_seqlen: int,
+                 lengths_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One call; ``lengths_out`` (work lists with kv_new: a contiguous int32
+        device tensor with one entry per row) receives each row's new length."""
         self.check(q, cache, out, kv_new)
         p = self.params
         p.q, p.cache, p.out = q.data_ptr(), cache.data_ptr(), out.data_ptr()
@@ -641,123 +737,124 @@ class AttendPlan:
         p.seqlen_bias, p.max_seqlen = int(seqlen_bias), int(max_seqlen)
         if self.lens is not None:
             self._use_work_list(seqlen_bias, max_seqlen)
-        _lib.check(self.lib.hexkv_attend(ctypes.byref(p), self.ws_ptr, self.ws_bytes, _stream(q)),
-                   "hexkv_attend")
+        if lengths_out is not None:
+            _require_device(lengths_out)
+            if lengths_out.dtype != torch.int32 or lengths_out.numel() < p.batch or not lengths_out.is_contiguous():
+                raise ValueError("lengths_out must be a contiguous int32 device tensor with one entry per row")
+            p.lengths_out_dev = lengths_out.data_ptr()
+        try:
+            rc = self.lib.hexkv_attend(ctypes.byref(p), self.ws_ptr, self.ws_bytes, _stream(q))
+        finally:
+            p.lengths_out_dev = None
+        _lib.check(rc, "hexkv_attend")
         return out
 
 
-class ReplayWorkLists:
-    """Work lists for a launch captured once and replayed over decode steps.
+class StepWorkLists:
+    """The work lists of consecutive decode steps, planned once on the host
+    and kept in one device buffer.
 
-    Replay k attends ``lens[b] + k + 1`` keys per row (``+ k`` without
-    ``kv_new``).  Every replay's list is cut with one chunk, the library's
-    choice for the last replay the lengths allow (``hexkv_attend_plan_chunk``),
-    so item and partition counts only grow over the replays and the last
-    replay's sizes -- the captured grid and workspace -- bound them all.
-    ``load(k)`` plans replay k on the host, pads the list to the captured
-    item count with items the kernels skip (row = batch, outside the call),
-    and copies it to fixed device buffers on the current stream; the host
-    buffers alternate, and one is rewritten only after its previous copy has
-    run.
+    Step t attends ``lens[b] + t + 1`` keys per row (``+ t`` without
+    ``kv_new``), for t < ``steps``; each step is planned with its own chunk
+    (``partition`` 0: the library's choice for that step, else the given
+    one) and, with ``single_launch``, for the device's XCDs.  ``self[t]`` is
+    step t's ``WorkList``; ``chunks[t]`` its chunk.  Nothing is planned or
+    copied per step afterwards.
     """
 
-    def __init__(self, p: _lib.AttendParams, lens: Sequence[int], max_seqlen: int, device):
-        self.lib = _lib.load()
+    def __init__(self, p: _lib.AttendParams, lens: Sequence[int], steps: int, device,
+                 single_launch: bool = True, partition: int = 0):
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("StepWorkLists must be built before graph capture")
+        lib = _lib.load()
         if len(lens) != p.batch:
             raise ValueError(f"{len(lens)} host lengths for a batch of {p.batch}")
+        if steps < 1:
+            raise ValueError("at least one step")
+        q = _lib.AttendParams.from_buffer_copy(p)
+        q.work_items_dev, q.work_parts_dev, q.lengths_out_dev = None, None, None
+        q.work_xcds = _plan_xcds(q, device, single_launch)
+        extra = 1 if q.kv_new else 0
         self.lens = [int(n) for n in lens]
-        self.extra = 1 if p.kv_new else 0
-        self.replays = int(max_seqlen) - max(self.lens, default=0) - self.extra + 1
-        if self.replays < 1:
-            raise ValueError(f"max_seqlen {max_seqlen} leaves no replay for lengths up to {max(self.lens)}")
-        self.params = _lib.AttendParams.from_buffer_copy(p)
-        q = self.params
-        q.max_seqlen, q.work_items_dev, q.work_parts_dev = int(max_seqlen), None, None
-        self.c_lens = (ctypes.c_int32 * len(self.lens))(*self.lens)
-        q.seqlen_bias = self.replays - 1
-        chunk = ctypes.c_int32()
-        _lib.check(self.lib.hexkv_attend_plan_chunk(ctypes.byref(q), self.c_lens, ctypes.byref(chunk)),
-                   "hexkv_attend_plan_chunk")
-        q.partition = chunk.value
-        n, mp = ctypes.c_int32(), ctypes.c_int32()
-        _lib.check(self.lib.hexkv_attend_plan(ctypes.byref(q), self.c_lens, None, 0, None, 0, ctypes.byref(n),
-                                              ctypes.byref(mp)), "hexkv_attend_plan")
-        self.chunk, self.capacity, self.max_parts = chunk.value, max(n.value, 1), mp.value
-        self.n_segs = max(p.batch * p.q_heads, 1)  # head groups never outnumber query heads
-        words = self.capacity * 8 + self.n_segs  # the items, then the partition counts
-        self.host = [torch.empty(words, dtype=torch.int32, pin_memory=True) for _ in range(2)]
-        self.copied = [torch.cuda.Event(), torch.cuda.Event()]
-        self.pending = [False, False]
-        self.dev = torch.empty(words, dtype=torch.int32, device=device)
-        self.work = WorkList(self.dev[:self.capacity * 8].view(self.capacity, 8), self.dev[self.capacity * 8:],
-                             self.capacity, self.max_parts)
-        for buf in self.host:
-            self._pad(buf, 0)
-        self.filled = [0, 0]  # items the last plan wrote into each host buffer
-        self.dev.copy_(self.host[0])
+        q.max_seqlen = max(self.lens, default=0) + steps - 1 + extra
+        c_lens = (ctypes.c_int32 * len(self.lens))(*self.lens)
+        n_segs = max(p.batch * p.q_heads, 1)  # head groups never outnumber query heads
+        sizes, self.chunks = [], []
+        for t in range(steps):
+            q.seqlen_bias = t
+            chunk, n, mp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+            q.partition = int(partition)
+            _lib.check(lib.hexkv_attend_plan_chunk(ctypes.byref(q), c_lens, ctypes.byref(chunk)),
+                       "hexkv_attend_plan_chunk")
+            q.partition = chunk.value
+            _lib.check(lib.hexkv_attend_plan(ctypes.byref(q), c_lens, None, 0, None, 0, ctypes.byref(n),
+                                             ctypes.byref(mp)), "hexkv_attend_plan")
+            sizes.append((max(n.value, 1), mp.value))
+            self.chunks.append(chunk.value)
+        # one buffer: per step, its items (8 words each) then n_segs counts
+        offsets, words = [], 0
+        for n, _ in sizes:
+            offsets.append(words)
+            words += n * 8 + n_segs + (-(n * 8 + n_segs) % 4)  # keep every items block 16-byte aligned
+        host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
+        base = host.data_ptr()
+        for t, ((n, _), off) in enumerate(zip(sizes, offsets)):
+            q.seqlen_bias, q.partition = t, self.chunks[t]
+            got, mp = ctypes.c_int32(), ctypes.c_int32()
+            _lib.check(lib.hexkv_attend_plan(ctypes.byref(q), c_lens, ctypes.c_void_p(base + off * 4), n,
+                                             ctypes.c_void_p(base + (off + n * 8) * 4), n_segs, ctypes.byref(got),
+                                             ctypes.byref(mp)), "hexkv_attend_plan")
+        self.device_buffer = host.to(device)
+        self.lists = [WorkList(self.device_buffer[off:off + n * 8].view(n, 8),
+                               self.device_buffer[off + n * 8:off + n * 8 + n_segs], n, mp, q.work_xcds)
+                      for (n, mp), off in zip(sizes, offsets)]
+        self.steps, self.xcds = steps, q.work_xcds
+        self.max_parts = max(mp for _, mp in sizes)
+        self.max_seqlen = q.max_seqlen
 
-    def _pad(self, buf: torch.Tensor, n: int) -> None:
-        items = buf[:self.capacity * 8].view(self.capacity, 8)
-        items[n:] = 0
-        items[n:, 0] = self.params.batch
+    def __len__(self) -> int:
+        return self.steps
 
-    def load(self, k: int) -> None:
-        if not 0 <= k < self.replays:
-            raise RuntimeError(f"work lists built for replays 0..{self.replays - 1}, asked for {k}")
-        i = k % 2
-        if self.pending[i]:
-            self.copied[i].synchronize()
-        buf = self.host[i]
-        q = self.params
-        q.seqlen_bias = k
-        n, mp = ctypes.c_int32(), ctypes.c_int32()
-        base = buf.data_ptr()
-        _lib.check(self.lib.hexkv_attend_plan(ctypes.byref(q), self.c_lens, ctypes.c_void_p(base), self.capacity,
-                                              ctypes.c_void_p(base + self.capacity * 32), self.n_segs,
-                                              ctypes.byref(n), ctypes.byref(mp)), "hexkv_attend_plan")
-        if mp.value > self.max_parts:
-            raise RuntimeError(f"replay {k} needs {mp.value} partitions, {self.max_parts} captured")
-        if n.value < self.filled[i]:  # counts only grow over replays; kept for any caller
-            self._pad(buf, n.value)
-        self.filled[i] = n.value
-        self.dev.copy_(buf, non_blocking=True)
-        self.copied[i].record()
-        self.pending[i] = True
+    def __getitem__(self, t: int) -> WorkList:
+        return self.lists[t]
 
 
 class DecodeStepGraph:
-    """One decode step's fused append + attend over every layer, captured once
-    as a HIP graph and replayed per step.
+    """One decode step's fused append + attend over every layer as a
+    captured HIP graph, replayed per step.
 
     ``positions`` (device int32 ``[B]``) holds each sequence's cached length.
-    A replay writes ``kv_new[l]`` at ``positions`` in every layer's cache,
-    attends ``positions + 1`` keys with ``q[l]`` into ``out[l]``, then
-    advances ``positions`` by one -- all inside the graph, so the host issues
-    one launch per step instead of two per layer.  ``max_seqlen`` bounds the
-    attended length over every replay (it sizes the grid and workspace).
-    This is the graph-captured decode step of hexgen_core's generation loop
+    A replay writes ``kv_new[l]`` at each sequence's position in every
+    layer's cache, attends the keys up to and including it with ``q[l]``
+    into ``out[l]``, and advances ``positions`` by one, all inside the graph:
+    the host issues one launch per step instead of one or two per layer.
+    ``max_seqlen`` bounds the attended length over every replay.  This is the
+    graph-captured decode step of hexgen_core's generation loop
     (hexgen/hexgen_core/generation.py:354-443) restricted to the KV path.
 
-    ``lens``, the host values of ``positions`` at the first replay, switches
-    the attention to work lists (``ReplayWorkLists``): each replay first
-    plans its step on the host and copies the list to the buffers the graph
-    reads, then launches the graph.  Replay k then attends ``lens + k + 1``
-    keys whatever ``positions`` holds (which still advances by one per
-    replay), and ``max_seqlen`` should be tight: the captured grid is the
-    item count of the last replay it allows.  ``step`` counts the replays.
-    ``partition`` sets the positions per partition (grid) or per item (work
-    list); 0 leaves it to the library.
+    Without ``lens`` the attention runs the library's uniform partitions over
+    the lengths in ``positions`` (one graph, positions advanced by a small
+    kernel after the last layer).  With ``lens``, the host values of
+    ``positions`` at the first replay, every step's work list is planned up
+    front (``StepWorkLists``, with ``single_launch`` for the device's XCDs)
+    and each step is its own captured graph over its own list, in which the
+    last layer's attention kernel also stores the new lengths to
+    ``positions``: a replay does no host planning, no copy and no extra
+    launch.  Replay k then attends ``lens + k + 1`` keys, and ``max_seqlen``
+    (which sets how many steps are captured) should be tight.  ``step``
+    counts the replays; ``partition`` sets the positions per partition (grid)
+    or per item (work lists); 0 leaves it to the library.
 
     The kernels must have run once eagerly in this process before capture
     (code objects load on first launch).  Graph nodes hold the tensors'
     addresses: the tensors must stay alive, and be updated in place, for as
-    long as the graph is replayed.
+    long as the graphs are replayed.
     """
 
     def __init__(self, q_layers: TensorList, cache_layers: TensorList, out_layers: TensorList,
                  kv_new_layers: TensorList, positions: torch.Tensor, max_seqlen: int,
                  softmax_scale: Optional[float] = None, kernel: str = "auto",
-                 lens: Optional[Sequence[int]] = None, partition: int = 0):
+                 lens: Optional[Sequence[int]] = None, partition: int = 0, single_launch: bool = True):
         self.q, self.cache = _as_layers(q_layers), _as_layers(cache_layers)
         self.out, self.kv_new = _as_layers(out_layers), _as_layers(kv_new_layers)
         if not (len(self.q) == len(self.cache) == len(self.out) == len(self.kv_new)) or not self.q:
@@ -773,20 +870,40 @@ class DecodeStepGraph:
         for l in range(len(self.q)):
             self.plan.check(self.q[l], self.cache[l], self.out[l], self.kv_new[l])
         self.lists = None
-        if lens is not None:
-            self.lists = ReplayWorkLists(self.plan.params, lens, self.max_seqlen, positions.device)
-            self.plan.fix_work_list(self.lists.work)
         self.step = 0
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            for l in range(len(self.q)):
-                self.plan(self.q[l], self.cache[l], self.out[l], self.kv_new[l], 0, self.max_seqlen)
-            self.positions.add_(1)
+        if lens is None:
+            self.graphs = [torch.cuda.CUDAGraph()]
+            with torch.cuda.graph(self.graphs[0]):
+                for l in range(len(self.q)):
+                    self.plan(self.q[l], self.cache[l], self.out[l], self.kv_new[l], 0, self.max_seqlen)
+                self.positions.add_(1)
+            return
+        steps = self.max_seqlen - max([int(n) for n in lens], default=0)
+        if steps < 1:
+            raise ValueError(f"max_seqlen {max_seqlen} leaves no step for lengths up to {max(lens)}")
+        self.lists = StepWorkLists(self.plan.params, lens, steps, positions.device, single_launch, partition)
+        self.plan.reserve(self.lists.lists)
+        self.graphs = []
+        pool = None
+        last = len(self.q) - 1
+        for t in range(steps):
+            self.plan.fix_work_list(self.lists[t])
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=pool):
+                for l in range(len(self.q)):
+                    self.plan(self.q[l], self.cache[l], self.out[l], self.kv_new[l], 0, self.max_seqlen,
+                              lengths_out=self.positions if l == last else None)
+            pool = graph.pool()
+            self.graphs.append(graph)
 
     def replay(self) -> None:
-        if self.lists is not None:
-            self.lists.load(self.step)
-        self.graph.replay()
+        if self.lists is None:
+            self.graphs[0].replay()
+        else:
+            if self.step >= len(self.graphs):
+                raise RuntimeError(f"work lists captured for replays 0..{len(self.graphs) - 1}, "
+                                   f"asked for {self.step}")
+            self.graphs[self.step].replay()
         self.step += 1
 
     def restart(self) -> None:

@@ -47,8 +47,8 @@ enum hexkv_dtype {
   HEXKV_F32 = 2   /* torch.float32  */
 };
 
-/* Attention kernels.  AUTO picks MFMA for 16-bit data with head_dim >= 64
- * and 8+ query heads per KV head, VALU otherwise. */
+/* Attention kernels.  AUTO picks MFMA for 16-bit data with head_dim 64 or
+ * 128 and 8+ query heads per KV head, VALU otherwise. */
 enum hexkv_kernel {
   HEXKV_KERNEL_AUTO = 0,
   HEXKV_KERNEL_VALU = 1, /* packed dot products on the vector ALUs     */
@@ -74,6 +74,36 @@ int hexkv_version(void);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char *hexkv_last_error(void);
+
+/*
+ * Device status flags: conditions a kernel met in values it read from device
+ * memory (which the host could not check before the launch), handled
+ * without a fault and recorded in one status word per GPU.
+ */
+#define HEXKV_STATUS_APPEND_SKIPPED 1u /* hexkv_append: a position outside [0, capacity); that row was not written */
+#define HEXKV_STATUS_LENGTH_CLAMPED 2u /* hexkv_attend / hexkv_ft_attend: a row length above max_seqlen, cut to it
+                                          (with kv_new, a new row past that bound was neither written nor attended) */
+#define HEXKV_STATUS_PLACEMENT 4u      /* hexkv_attend: the items of a split segment ran on more than one XCD
+                                          (work_xcds > 0), so its in-kernel merge may have read stale partials */
+#define HEXKV_STATUS_DISPATCH 8u       /* hexkv_attend, information only: a work item ran on another XCD than its
+                                          index modulo work_xcds (the segment's items can still share one) */
+
+/*
+ * Waits for `stream`, then reads the status word of the stream's device into
+ * *flags (HEXKV_STATUS_* bits) and, when `clear` is nonzero, resets it.  Not
+ * for use under graph capture (it synchronises).
+ *
+ * The reference checks the append position on the host before every write
+ * (assert sequence_end <= kv_cache.shape[1], hexgen/hexgen_core/modules/
+ * mha.py:281-282) because its offset is a host integer; with per-sequence
+ * positions in device memory the check happens in the kernels, and this
+ * call reports it at the caller's next synchronisation point.
+ */
+int hexkv_device_status(uint32_t *flags, int clear, hexkv_stream_t stream);
+
+/* Number of XCDs (dies with their own L2) of the current HIP device, for
+ * hexkv_attend_params.work_xcds.  No counterpart in the reference. */
+int hexkv_device_xcds(int32_t *xcds);
 
 /*
  * Pack: for every layer l < n_layers and sequence b < batch, copy rows
@@ -118,8 +148,9 @@ int hexkv_unpack(const void *const *packed_layers, void *const *cache_layers,
  * Append: for every sequence b < batch, copy row b of kv_new ([batch][row],
  * contiguous) into the cache at position
  *   pos_b = (positions_dev ? positions_dev[b] : 0) + position_bias.
- * Rows with pos_b outside [0, capacity) are skipped on the device (the host
- * wrapper rejects them first whenever positions are known on the host).
+ * Rows with pos_b outside [0, capacity) are skipped on the device and raise
+ * HEXKV_STATUS_APPEND_SKIPPED (the host wrapper rejects them first whenever
+ * positions are known on the host).
  *
  * Replaces the slice assignment of _update_kv_cache,
  *   kv_cache[batch_start:batch_end, sequence_start:sequence_end, ...] = kv
@@ -197,11 +228,29 @@ typedef struct hexkv_attend_params {
   const int32_t *work_parts_dev;
   int32_t n_work_items;
   int32_t work_max_parts;
+  /* XCDs the work list is planned for (hexkv_attend_plan reads it too).
+   * 0: the partials of a split (row, head group) are merged by a second
+   * kernel on the same stream.  N > 0 (the device's XCD count,
+   * hexkv_device_xcds): every item of a split segment sits at one index
+   * modulo N, so -- workgroups reach the N XCDs round-robin by index -- its
+   * items share one XCD's L2, and the segment's last item to finish merges
+   * the partials inside the attention kernel: one launch per call.  Each
+   * workgroup checks its XCD and raises HEXKV_STATUS_PLACEMENT otherwise. */
+  int32_t work_xcds;
+  /* Work-list calls with kv_new only, else NULL: row b's new cached length
+   * (its attended keys, the appended row included) is stored to
+   * lengths_out_dev[b], so a captured decode step advances the caller's
+   * lengths in the same launch. */
+  int32_t *lengths_out_dev;
 } hexkv_attend_params;
 
 /* Workspace bytes hexkv_attend needs for these parameters (0 when one
  * partition covers every sequence).  The workspace is scratch (partial
- * outputs of the split-K merge); calls sharing one must not overlap. */
+ * outputs of the split-K merge) behind HEXKV_ATTEND_COUNTER_BYTES of
+ * arrival counters, which single-launch merges (work_xcds > 0) use and
+ * leave zero: zero the workspace once after allocating it.  Calls sharing
+ * one workspace must not overlap. */
+#define HEXKV_ATTEND_COUNTER_BYTES (256u << 10)
 size_t hexkv_attend_workspace_bytes(const hexkv_attend_params *p);
 
 /* The kernel hexkv_attend runs for these parameters, HEXKV_KERNEL_VALU or
@@ -233,9 +282,13 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
  * bytes the call reads, see hexkv_attend_plan_chunk; else a multiple of 64),
  * and the items are ordered for the launch: empty
  * rows, then the full chunks across all segments, then each segment's last,
- * shorter chunk from the longest down.  Host memory only; the caller copies
- * `items` and `parts` to the device and passes them in
- * hexkv_attend_params.work_*.
+ * shorter chunk from the longest down.  With p->work_xcds = N > 0 the
+ * segments are first dealt to the N XCDs (longest first, each to the XCD with
+ * the fewest positions so far), that order is kept within each XCD's items,
+ * and XCD x's j-th item goes to index j * N + x; shorter XCD lists are padded
+ * with items the kernels skip (row = batch), so n_items is a multiple of N.
+ * Host memory only; the caller copies `items` and `parts` to the device and
+ * passes them in hexkv_attend_params.work_*.
  *
  *   lens            host int32 [batch]
  *   items, parts    host outputs: up to items_capacity items and

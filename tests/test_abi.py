@@ -202,3 +202,38 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         ops.attend_kernel(torch.zeros((1, 1, 8, 64), dtype=torch.float16),
                           torch.zeros((1, 4, 2, 1, 64), dtype=torch.float16))
+
+
+def test_empty_batch_with_a_work_list_launches_nothing():
+    """An empty batch plans an empty list and the call returns HEXKV_OK
+    without launching, with or without a work list (no GPU needed: nothing
+    reaches the runtime)."""
+    lib = _lib.load()
+    p = _lib.AttendParams(dtype=1, batch=0, q_len=1, q_heads=8, kv_heads=2, head_dim=64, capacity=8,
+                          max_seqlen=4, softmax_scale=0.125)
+    n, mp = ctypes.c_int32(), ctypes.c_int32()
+    lens = (ctypes.c_int32 * 1)()
+    assert lib.hexkv_attend_plan(ctypes.byref(p), lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)) == 0
+    assert n.value == 0
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_OK
+    p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds = 256, 256, 0, 1, 8
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_OK
+    assert lib.hexkv_last_error() == b""
+
+
+def test_single_launch_and_lengths_out_validation():
+    """work_xcds and lengths_out_dev are checked before any launch."""
+    lib = _lib.load()
+    p = _lib.AttendParams(dtype=1, batch=1, q_len=1, q_heads=8, kv_heads=2, head_dim=64, capacity=8,
+                          max_seqlen=4, softmax_scale=0.125, q=256, cache=256, out=256,
+                          cache_batch_stride=8 * 2 * 2 * 64, cache_pos_stride=2 * 2 * 64, cache_kv_stride=128)
+    p.work_xcds = 8  # without a work list
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_EINVAL
+    assert b"work lists" in lib.hexkv_last_error()
+    p.work_xcds = 65
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_EINVAL
+    p.work_xcds, p.lengths_out_dev = 0, 256  # lengths_out without a work list and kv_new
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_EINVAL
+    assert b"lengths_out_dev" in lib.hexkv_last_error()
+    assert lib.hexkv_device_status(None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_device_xcds(None) == _lib.HEXKV_EINVAL

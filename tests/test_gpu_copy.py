@@ -162,6 +162,10 @@ def test_append_per_sequence_positions(device, dtype):
 
 
 def test_append_out_of_range_rows_are_skipped_on_device(device):
+    """Positions read on the device outside [0, capacity) are not written,
+    and the status word reports it (ValueError at the next check); an
+    in-range append leaves the status clear."""
+    ops.device_status()  # start clear
     cache = torch.zeros((3, 4, 2, 1, 8), dtype=torch.float16, device=device)
     kv = torch.ones((3, 2, 1, 8), dtype=torch.float16, device=device)
     ops.append_kv(cache, kv, torch.tensor([4, -1, 2], dtype=torch.int32, device=device))
@@ -169,6 +173,10 @@ def test_append_out_of_range_rows_are_skipped_on_device(device):
     got = cache.cpu()
     assert (got[0] == 0).all() and (got[1] == 0).all()
     assert (got[2, 2] == 1).all() and got[2].sum() == 16
+    with pytest.raises(ValueError, match="append position"):
+        ops.check_device_status()
+    ops.append_kv(cache, kv, torch.tensor([3, 0, 1], dtype=torch.int32, device=device))
+    ops.check_device_status()  # cleared by the check above; nothing new
 
 
 def test_host_validation_rejects_bad_lengths_before_launch(device):

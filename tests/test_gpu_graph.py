@@ -3,13 +3,14 @@
 Every replay is compared with the eager fused append+attend of the same
 step (same kernels and partitions, so bit-exact), with fresh q/kv_new
 written in place and eager work plus synchronisation between replays; one
-step is also checked against the float64 oracle.  The work-list graph is
-compared the same way with the eager work-list calls."""
+step is also checked against the float64 oracle.  The work-list graphs (one
+per step, lists planned up front) are compared the same way with the eager
+work-list calls; planning a list under capture is refused."""
 import numpy as np
 import pytest
 import torch
 
-from hexgen2_amd import ops
+from hexgen2_amd import _lib, ops
 from oracle import kv_oracle as oracle
 
 pytestmark = pytest.mark.gpu
@@ -66,17 +67,23 @@ def test_graph_replays_match_eager_steps(device, hq, hkv, d, dtype, kernel):
             assert changed.sum() <= len(lens)
 
 
-@pytest.mark.parametrize("hq,hkv,d,dtype,kernel,partition", [(32, 8, 128, torch.bfloat16, "valu", 64),
-                                                             (32, 8, 128, torch.bfloat16, "mfma", 128),
-                                                             (8, 1, 128, torch.bfloat16, "auto", 0),
-                                                             (32, 4, 64, torch.float16, "auto", 64),
-                                                             (4, 4, 16, torch.float32, "auto", 64)])
-def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, kernel, partition):
-    """DecodeStepGraph(lens=...): each replay uploads its step's work list
-    into the buffers the graph captured (padded to the last replay's item
-    count) and equals, bit for bit, the eager work-list call of the same
-    step with the same chunk; rows cross chunk boundaries during the
-    replays, so item and partition counts grow under the fixed capture."""
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel,partition,single", [
+    (32, 8, 128, torch.bfloat16, "valu", 64, True),
+    (32, 8, 128, torch.bfloat16, "mfma", 128, True),
+    (32, 8, 128, torch.bfloat16, "valu", 64, False),
+    (8, 1, 128, torch.bfloat16, "auto", 0, True),
+    (32, 4, 64, torch.float16, "auto", 0, True),
+    (32, 4, 64, torch.float16, "auto", 64, False),
+    (4, 4, 16, torch.float32, "auto", 64, True)])
+def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, kernel, partition, single):
+    """DecodeStepGraph(lens=...): every step's work list is planned up front
+    (StepWorkLists) and captured in a graph of its own, and the last layer's
+    kernel stores the new lengths to ``positions``; each replay equals, bit
+    for bit, the eager work-list calls of the same step with the same chunk
+    (merged in the attention kernel, or by the second kernel), with fresh q
+    and kv_new written in place and eager work between the replays.  Rows
+    cross chunk boundaries during the replays, so item and partition counts
+    change from graph to graph."""
     # after the eager step, replay k attends lens + k + 2 keys: sequence 2
     # crosses 384 (a multiple of 64 and 128) at k = 1, sequence 4 crosses 64
     layers, lens, steps = 3, [1, 40, 381, 1029, 62], 6
@@ -95,7 +102,7 @@ def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, ke
     def eager_step(chunk):
         for l in range(layers):
             ops.decode_attention(q[l], cache_e[l], max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[l],
-                                 out=out_e[l], kernel=kernel, lens=host, partition=chunk)
+                                 out=out_e[l], kernel=kernel, lens=host, partition=chunk, single_launch=single)
         pos_e.add_(1)
         host[:] = [n + 1 for n in host]
 
@@ -103,32 +110,59 @@ def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, ke
         q.copy_(torch.randn(q.shape, generator=g, device=device).to(dtype))
         kv_new.copy_(torch.randn(kv_new.shape, generator=g, device=device).to(dtype))
 
+    ops.device_status()  # start clear
     refill()
     eager_step(partition)  # also loads the kernels before capture
     cache_g.copy_(cache_e)
     pos_g = pos_e.clone()
     torch.cuda.synchronize()
     graph = ops.DecodeStepGraph(q, cache_g, out_g, kv_new, pos_g, max_seqlen, kernel=kernel, lens=host,
-                                partition=partition)
+                                partition=partition, single_launch=single)
     lists = graph.lists
-    assert lists.replays == steps - 1
+    assert len(lists) == steps - 1 and (lists.xcds > 0) == single
     if partition:
-        assert lists.chunk == partition
+        assert set(lists.chunks) == {partition}
     counts = []
     for step in range(steps - 1):
         refill()
-        eager_step(lists.chunk)
+        eager_step(lists.chunks[step])
         graph.replay()
         torch.cuda.synchronize()
-        counts.append(lists.filled[step % 2])
-        assert torch.equal(pos_g, pos_e)
+        counts.append(int(lists[step].parts.sum()))  # partitions over all segments
+        assert torch.equal(pos_g, pos_e), f"step {step}: positions differ"
         assert torch.equal(cache_g, cache_e), f"step {step}: cache differs"
         assert torch.equal(out_g, out_e), f"step {step}: output differs"
-    assert counts == sorted(counts) and counts[-1] == lists.capacity
     if partition:
         assert counts[0] < counts[-1], "a row crossed a chunk boundary during the replays"
+    status = ops.device_status()
+    print(f"  device status {status:#x}", flush=True)
+    assert status & _lib.STATUS_ERRORS == 0
     with pytest.raises(RuntimeError, match="replays"):
         graph.replay()  # past the last length max_seqlen allows
+    graph.restart()
+    assert graph.step == 0
+
+
+def test_planning_under_capture_is_refused(device):
+    """A work list planned inside graph capture would record a copy from a
+    temporary host buffer: decode_attention(lens=...) and AttendPlan(lens=...)
+    raise ValueError there, and leave the stream usable."""
+    q = torch.randn((2, 1, 8, 64), device=device).to(torch.float16)
+    cache = torch.randn((2, 64, 2, 2, 64), device=device).to(torch.float16)
+    out = torch.empty_like(q)
+    seqlens = torch.tensor([10, 20], dtype=torch.int32, device=device)
+    ops.decode_attention(q, cache, max_seqlen=21, seqlens=seqlens, out=out, lens=[10, 20])  # loads the kernel
+    torch.cuda.synchronize()
+    plan = ops.AttendPlan(q, cache, out, max_seqlens=[21], seqlens=seqlens, lens=[10, 20])
+    for call in (lambda: ops.decode_attention(q, cache, max_seqlen=21, seqlens=seqlens, out=out, lens=[10, 20]),
+                 lambda: plan(q, cache, out, None, 0, 21)):
+        graph = torch.cuda.CUDAGraph()
+        with pytest.raises(ValueError, match="graph capture"):
+            with torch.cuda.graph(graph):
+                call()
+        torch.cuda.synchronize()
+    ops.decode_attention(q, cache, max_seqlen=21, seqlens=seqlens, out=out, lens=[10, 20])
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("hq,hkv,d,dtype,rot", [(32, 8, 128, torch.bfloat16, 128),

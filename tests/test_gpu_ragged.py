@@ -154,3 +154,59 @@ def test_ragged_batch_decode_equals_decoding_alone(device, dtype, fused):
         for b, (tokens, want_logits, _) in enumerate(alone):
             assert int(token[b]) == tokens[step], (b, step)
             torch.testing.assert_close(logits[b], want_logits[step], atol=0.03, rtol=0.03)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_lengths_past_the_offset_are_reported(device, fused):
+    """lengths_per_sample[b] > sequence_len_offset breaks the ragged contract
+    (the attended view ends at the offset).  The reference would assert on
+    the host (mha.py:281-282); here every kernel exits normally, row b is cut
+    to the view (so its own new key is missed) and the status word reports
+    it: mha.check_kv_status raises ValueError at the caller's next check.
+    In-contract steps before and after leave it clear."""
+    from hexgen2_amd.mha import check_kv_status
+
+    dtype, hq, hkv, d = torch.float16, 8, 2, 64
+    g = torch.Generator(device=device).manual_seed(5)
+    cap = 64
+    cache = torch.randn((3, cap, 2, hkv, d), generator=g, device=device).to(dtype)
+    ops.device_status()  # start clear
+
+    def step(lens, offset):
+        lengths = torch.tensor(lens, dtype=torch.int32, device=device)
+        params = InferenceParams(max_sequence_len=cap, max_batch_size=3, sequence_len_offset=offset,
+                                 key_value_memory_dict={0: cache}, lengths_per_sample=lengths)
+        q = torch.randn((3, 1, hq, d), generator=g, device=device).to(dtype)
+        kv = torch.randn((3, 1, 2, hkv, d), generator=g, device=device).to(dtype)
+        if fused:
+            out = update_and_attend(q, kv, params, 0)
+        else:
+            out = FlashCrossAttention(causal=True)(q, _update_kv_cache(kv, params, 0), causal=False)
+        torch.cuda.synchronize()
+        return out
+
+    step([5, 9, 12], 12)
+    check_kv_status()  # in contract: nothing raised
+    out = step([5, 30, 12], 12)  # row 1 sits past the offset
+    assert torch.isfinite(out.float()).all()
+    with pytest.raises(ValueError, match="exceeded the attended view"):
+        check_kv_status()
+    step([6, 10, 13], 13)
+    check_kv_status()  # the check cleared the flag
+
+
+def test_prompt_step_ignores_lengths_per_sample(device):
+    """At sequence_len_offset 0 (the prompt) _update_kv_cache writes at the
+    offset even when lengths_per_sample is set -- the reference's generation
+    loop fills it with the prompt lengths before the prompt's forward
+    (generation.py:380) -- so a one-token prompt lands at position 0."""
+    dtype, hkv, d = torch.float16, 2, 64
+    cache = torch.zeros((2, 16, 2, hkv, d), dtype=dtype, device=device)
+    params = InferenceParams(max_sequence_len=16, max_batch_size=2, sequence_len_offset=0,
+                             key_value_memory_dict={0: cache},
+                             lengths_per_sample=torch.tensor([1, 1], dtype=torch.int32, device=device))
+    kv = torch.ones((2, 1, 2, hkv, d), dtype=dtype, device=device)
+    view = _update_kv_cache(kv, params, 0)
+    torch.cuda.synchronize()
+    assert view.shape[1] == 1
+    assert (cache[:, 0] == 1).all() and (cache[:, 1:] == 0).all()

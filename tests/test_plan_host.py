@@ -9,7 +9,9 @@
   every attended position of every (row, head group) exactly once, the
   partition numbers and counts agree with the merge's view, the order is
   empty rows, full chunks, then the shorter last chunks from the longest
-  down, and the library's chunk choice follows its three regimes.
+  down, and the library's chunk choice follows its three regimes; planned
+  for the device's XCDs, every item of a split (row, head group) sits at one
+  index modulo the XCD count, with the same order within each XCD.
 """
 import ctypes
 
@@ -284,28 +286,110 @@ def test_random_plans(seed):
     assert arr[:, 5].max() <= chunk
 
 
-@pytest.mark.parametrize("seed", range(12))
-def test_counts_only_grow_over_replays_at_a_fixed_chunk(seed):
-    """The property a captured decode graph relies on: with the chunk fixed
-    (the last replay's, as ReplayWorkLists chooses it), every replay's item
-    count and largest partition count are at most the next one's, so the
-    last replay's sizes bound the capture."""
-    rng = np.random.default_rng(8000 + seed)
-    hkv = int(rng.choice([1, 4, 8]))
-    hq = hkv * int(rng.choice([1, 4, 8]))
-    batch = int(rng.integers(1, 40))
-    lens = [int(x) for x in rng.integers(1, 6000, batch)]
-    replays = int(rng.integers(2, 80))
-    max_seqlen = max(lens) + replays  # replay k attends lens + k + 1 keys
-    last = params(batch, hq, hkv, 128, bias=replays - 1, max_seqlen=max_seqlen)
-    rc, chunk = plan_chunk(last, lens)
+def check_xcd_plan(arr, parts, lens, hq, hkv, xcds, bias=0, extra=1):
+    """A plan for ``xcds`` XCDs: the real items cover every position once;
+    every item of one (row, head group) sits at one index modulo ``xcds``
+    (so they run on one XCD); each XCD's items keep the dispatch order;
+    padding items (row = batch, all else zero) only end an XCD's share; the
+    XCDs' positions differ by at most one segment's."""
+    batch = len(lens)
+    assert len(arr) % xcds == 0
+    pad = arr[:, 0] == batch
+    assert (arr[pad][:, 1:] == 0).all()
+    check_cover(arr[~pad], parts, lens, hq, hkv, bias=bias, extra=extra)
+    homes = {}
+    for i in np.nonzero(~pad)[0]:
+        homes.setdefault((int(arr[i, 0]), int(arr[i, 1])), set()).add(int(i) % xcds)
+    assert all(len(h) == 1 for h in homes.values()), "a segment's items span XCDs"
+    load = np.zeros(xcds, dtype=np.int64)
+    for x in range(xcds):
+        share = arr[x::xcds]
+        col = share[:, 0] == batch
+        if col.any():
+            assert col[int(np.argmax(col)):].all(), "padding only at the end of an XCD's share"
+        check_order(share[~col])
+        load[x] = share[~col][:, 5].sum()
+    # segments are dealt longest first to the least loaded XCD: the loads end
+    # within one segment of each other
+    assert load.max() - load.min() <= max(max(n + bias + extra for n in lens), 1)
+
+
+@pytest.mark.parametrize("lens,hq,hkv,d", [
+    ([7897, 221, 4000, 1023, 1024, 1025, 0, 5000], 32, 8, 128),   # Llama-3-8B geometry, ragged
+    ([3806, 538, 2000], 8, 1, 128),                                # Llama-2-70B TP-8 share
+    ([512], 32, 4, 64),                                            # TinyLlama
+    ([100, 0, 3], 4, 4, 16),
+])
+@pytest.mark.parametrize("xcds", [1, 2, 8])
+def test_xcd_plans(lens, hq, hkv, d, xcds):
+    p = params(len(lens), hq, hkv, d)
+    p.work_xcds = xcds
+    rc, chunk = plan_chunk(p, lens)
     assert rc == 0
+    arr, parts, mp = plan(p, lens)
+    check_xcd_plan(arr, parts, lens, hq, hkv, xcds)
+    # the same chunks as a plain plan cut at that chunk
+    flat, flat_parts, flat_mp = plan(params(len(lens), hq, hkv, d, partition=chunk), lens)
+    assert np.array_equal(parts, flat_parts) and mp == flat_mp
+    if xcds == 1:
+        assert np.array_equal(arr, flat), "one XCD: the plain order"
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_xcd_plans(seed):
+    """Random geometries and lengths planned for 8 XCDs (and for a random
+    count up to 64): the placement, cover and order rules of check_xcd_plan."""
+    rng = np.random.default_rng(9000 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([1, 2, 4, 8]))
+    hq, d = hkv * group, int(rng.choice([64, 128]))
+    batch = int(rng.integers(1, 70))
+    lens = [int(x) for x in rng.integers(0, 9000, batch)]
+    kv_new = bool(rng.integers(2))
+    extra = 1 if kv_new else 0
+    partition = int(rng.choice([0, 0, 64, 320, 1280]))
+    for xcds in (8, int(rng.integers(2, 65))):
+        p = params(batch, hq, hkv, d, max_seqlen=max(lens) + extra, kv_new=kv_new, partition=partition)
+        p.work_xcds = xcds
+        arr, parts, _ = plan(p, lens)
+        check_xcd_plan(arr, parts, lens, hq, hkv, xcds, extra=extra)
+
+
+def test_xcd_plan_rejects_bad_counts():
     lib = _lib.load()
-    c_lens = (ctypes.c_int32 * batch)(*lens)
-    sizes = []
-    for k in range(replays):
-        p = params(batch, hq, hkv, 128, bias=k, max_seqlen=max_seqlen, partition=chunk)
-        n, mp = ctypes.c_int32(), ctypes.c_int32()
-        assert lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)) == 0
-        sizes.append((n.value, mp.value))
-    assert all(a[0] <= b[0] and a[1] <= b[1] for a, b in zip(sizes, sizes[1:]))
+    n, mp = ctypes.c_int32(), ctypes.c_int32()
+    lens = (ctypes.c_int32 * 2)(10, 20)
+    for bad in (-1, 65):
+        p = params(2, 8, 2, 64)
+        p.work_xcds = bad
+        assert lib.hexkv_attend_plan(ctypes.byref(p), lens, None, 0, None, 0, ctypes.byref(n),
+                                     ctypes.byref(mp)) == _lib.HEXKV_EINVAL
+    # more (row, head group) segments than the merge has counters for
+    many = 20000
+    big = (ctypes.c_int32 * many)(*([1] * many))
+    p = params(many, 8, 8, 64)  # 8 segments per row
+    assert lib.hexkv_attend_plan(ctypes.byref(p), big, None, 0, None, 0, ctypes.byref(n),
+                                 ctypes.byref(mp)) == _lib.HEXKV_OK
+    p.work_xcds = 8
+    assert lib.hexkv_attend_plan(ctypes.byref(p), big, None, 0, None, 0, ctypes.byref(n),
+                                 ctypes.byref(mp)) == _lib.HEXKV_EINVAL
+    assert b"segments" in lib.hexkv_last_error()
+
+
+def test_small_calls_split_when_merged_in_kernel():
+    """Below 4 MB read a call is one item per segment with a second-kernel
+    merge (the merge launch would cost more than the split saves), but split
+    into pieces of about a twelfth of the longest row, 64 positions at least,
+    when planned for the XCDs (merged in the attention kernel)."""
+    p = params(1, 32, 4, 64, dtype=_lib.HEXKV_F16)
+    arr, _, mp = plan(p, [576])
+    assert mp == 1 and len(arr) == 4
+    p.work_xcds = 8
+    rc, chunk = plan_chunk(p, [576])
+    assert rc == 0 and chunk == 64
+    arr, parts, mp = plan(p, [576])
+    assert mp == 10 and (parts[:4] == 10).all()
+    check_xcd_plan(arr, parts, [576], 32, 4, 8)
+    assert len(arr) == 80  # 4 XCDs with one segment's 10 items, 4 with padding only
+    rc, chunk = plan_chunk(p, [4000])
+    assert rc == 0 and chunk == 384

@@ -2,13 +2,15 @@
 hexkv_attend (caller's workspace), both called through the C ABI.
 
 The two entry points run the same kernels with the same partitioning (the
-library's grid, or one host-planned work list for both), so their outputs
-must agree bit for bit (and the fused append must write the
-same cache bytes); each output is also checked against the float64 oracle
-(bf16 8e-3, fp16 2e-3 max-abs).  Two calls in a row, the second with fewer
-rows and shorter lengths, so stale partials of the first call in the shared
-scratch would show.  A request beyond the scratch is refused with
-HEXKV_EWORKSPACE before anything is launched.
+library's grid, or one host-planned work list for both, its split rows
+merged by a second kernel or, planned for the device's XCDs, inside the
+attention kernel with arrival counters at the front of the workspace / the
+scratch), so their outputs must agree bit for bit (and the fused append must
+write the same cache bytes); each output is also checked against the float64
+oracle (bf16 8e-3, fp16 2e-3 max-abs).  Two calls in a row, the second with
+fewer rows and shorter lengths, so stale partials or counters of the first
+call in the shared scratch would show.  A request beyond the scratch is
+refused with HEXKV_EWORKSPACE before anything is launched.
 """
 import ctypes
 
@@ -32,11 +34,13 @@ def stream_of(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def both(q, cache, lens, kv_new, kernel, listed=False):
+def both(q, cache, lens, kv_new, kernel, listed=None):
     """(workspace output, no-alloc output, cache after each) of one call;
-    ``listed``: both calls run the same host-planned work list of
-    128-position items (its device buffers are the caller's inputs)."""
+    ``listed`` "xcd" or "two-launch": both calls run the same host-planned
+    work list of 128-position items (its device buffers are the caller's
+    inputs), merged in the attention kernel or by a second one."""
     lib = _lib.load()
+    ops.device_status()  # clear flags earlier tests may have raised on purpose
     seqlens = torch.tensor(lens, dtype=torch.int32, device=q.device)
     max_seqlen = max(lens) + 1
     c_ws, c_na = cache.clone(), cache.clone()
@@ -44,12 +48,13 @@ def both(q, cache, lens, kv_new, kernel, listed=False):
     # The work list is cut into 128-position chunks so that both calls split.
     p = ops._attend_params(q, c_ws, o_ws, seqlens, 0, max_seqlen, kv_new, False, None, 128 if listed else 0,
                            kernel)
-    work = ops._plan_work(p, lens, q.device) if listed else None
+    work = ops._plan_work(p, lens, q.device, single_launch=listed == "xcd") if listed else None
     if work:
         work.apply(p)
+        assert (work.xcds > 0) == (listed == "xcd")
     need = lib.hexkv_attend_workspace_bytes(ctypes.byref(p))
     assert 0 < need <= _lib.NOALLOC_SCRATCH_BYTES
-    ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws = torch.zeros(need, dtype=torch.uint8, device=q.device)  # counters zero before first use
     _lib.check(lib.hexkv_attend(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need, stream_of(q)),
                "hexkv_attend")
     p = ops._attend_params(q, c_na, o_na, seqlens, 0, max_seqlen, kv_new, False, None, 0, kernel)
@@ -57,10 +62,13 @@ def both(q, cache, lens, kv_new, kernel, listed=False):
         work.apply(p)
     _lib.check(lib.hexkv_attend_noalloc(ctypes.byref(p), stream_of(q)), "hexkv_attend_noalloc")
     torch.cuda.synchronize()
+    status = ops.device_status()
+    print(f"  device status {status:#x}", flush=True)
+    assert status & _lib.STATUS_ERRORS == 0
     return o_ws, o_na, c_ws, c_na
 
 
-@pytest.mark.parametrize("listed", [False, True], ids=["grid", "work_list"])
+@pytest.mark.parametrize("listed", [None, "two-launch", "xcd"], ids=["grid", "work_list", "xcd_work_list"])
 @pytest.mark.parametrize("dtype,hq,hkv,d,kernel", [(torch.bfloat16, 32, 8, 128, "valu"),
                                                    (torch.bfloat16, 8, 1, 128, "mfma"),
                                                    (torch.float16, 32, 4, 64, "mfma")])

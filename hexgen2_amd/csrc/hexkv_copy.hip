@@ -134,6 +134,22 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(
 
 // ------------------------------------------------------------------ host ---
 
+// The status word of each GPU (HEXKV_STATUS_* bits, raised by kernels with
+// atomicOr), defined beside kernels so that its code object is one the
+// runtime loads with them.  Host code passes kernels the per-device address
+// that hipGetSymbolAddress returns, never the name itself.
+static __device__ unsigned int device_status;
+static std::atomic<void *> g_status_addr[kMaxDevices];
+
+int status_word(hexkv_stream_t stream, unsigned int **word, const char *what) {
+  void *ptr = nullptr;
+  const int rc = symbol_address(reinterpret_cast<const void *>(&HIP_SYMBOL(device_status)), g_status_addr, stream,
+                                &ptr, what);
+  *word = static_cast<unsigned int *>(ptr);
+  return rc;
+}
+
+
 // Packed bytes per workgroup: large enough to amortise the per-workgroup
 // sequence search, small enough to give every CU many workgroups.
 static int64_t choose_chunk(int64_t total_bytes) {
@@ -288,4 +304,21 @@ extern "C" int hexkv_append(const void *kv_new, void *cache, int batch, int64_t 
     append_kernel<unsigned int><<<grid, kAppendThreads, 0, s>>>(static_cast<const char *>(kv_new),
         static_cast<char *>(cache), stride, capacity, row_bytes, positions_dev, position_bias, status);
   return check_launch("hexkv_append");
+}
+
+extern "C" int hexkv_device_status(uint32_t *flags, int clear, hexkv_stream_t stream) {
+  using namespace hexkv;
+  clear_error();
+  const char *what = "hexkv_device_status";
+  if (!flags) return fail(HEXKV_EINVAL, "%s: null argument", what);
+  unsigned int *word = nullptr;
+  int rc = status_word(stream, &word, what);
+  if (rc != HEXKV_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipStreamSynchronize(s);
+  if (e == hipSuccess) e = hipMemcpyAsync(flags, word, sizeof(*flags), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && clear) e = hipMemsetAsync(word, 0, sizeof(*word), s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return HEXKV_OK;
 }

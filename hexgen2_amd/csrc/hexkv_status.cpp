@@ -1,5 +1,5 @@
-// Per-thread error reporting, version, the per-GPU device status word and the
-// device queries of the hexkv C ABI.
+// Per-thread error reporting, version, the per-device symbol lookup and the
+// device queries of the hexkv C ABI (host code only).
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -67,42 +67,11 @@ int symbol_address(const void *symbol, std::atomic<void *> *cache, hexkv_stream_
   return HEXKV_OK;
 }
 
-// The status word of each GPU (HEXKV_STATUS_* bits, raised by kernels with
-// atomicOr).  Host code passes kernels the per-device address that
-// hipGetSymbolAddress returns, never the name itself.
-static __device__ unsigned int device_status;
-static std::atomic<void *> g_status_addr[kMaxDevices];
-
-int status_word(hexkv_stream_t stream, unsigned int **word, const char *what) {
-  void *ptr = nullptr;
-  const int rc = symbol_address(reinterpret_cast<const void *>(&HIP_SYMBOL(device_status)), g_status_addr, stream,
-                                &ptr, what);
-  *word = static_cast<unsigned int *>(ptr);
-  return rc;
-}
-
 }  // namespace hexkv
 
 extern "C" int hexkv_version(void) { return 200; /* 0.2.0 */ }
 
 extern "C" const char *hexkv_last_error(void) { return hexkv::g_last_error; }
-
-extern "C" int hexkv_device_status(uint32_t *flags, int clear, hexkv_stream_t stream) {
-  using namespace hexkv;
-  clear_error();
-  const char *what = "hexkv_device_status";
-  if (!flags) return fail(HEXKV_EINVAL, "%s: null argument", what);
-  unsigned int *word = nullptr;
-  int rc = status_word(stream, &word, what);
-  if (rc != HEXKV_OK) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = hipStreamSynchronize(s);
-  if (e == hipSuccess) e = hipMemcpyAsync(flags, word, sizeof(*flags), hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess && clear) e = hipMemsetAsync(word, 0, sizeof(*word), s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: %s", what, hipGetErrorString(e));
-  return HEXKV_OK;
-}
 
 extern "C" int hexkv_device_xcds(int32_t *xcds) {
   using namespace hexkv;

@@ -208,7 +208,7 @@ class Pilot:
                   "start": t0, "prefill_end": t1, "send_end": t2, "end": t3,
                   "prefill_ms": elapsed_ms(t0, t1), "send_ms": elapsed_ms(t1, t2),
                   "roundtrip_ms": elapsed_ms(t0, t3), "decode": reply, "status": "success",
-                  "timing_note": "serial pilot: no streaming client, no throughput-serving claim"}
+                  "timing_note": "requests run one after another; latencies are per request, not serving throughput"}
         if self.args.check_colocated:
             # The same engine without a handoff must produce the same tokens.
             f, c, _ = self.engine.prefill(req.input_ids, req.max_new_tokens)
@@ -251,7 +251,7 @@ class Pilot:
         digests = [None, None]
         dist.all_gather_object(digests, self.settings_digest())
         if digests[0] != digests[1]:
-            raise ValueError("Ranks disagree on workload, model config, or run settings")
+            raise ValueError("the prefill and decode ranks were started with different traces, models or settings")
         (self.args.output / f"rank-{self.rank}-workload.json").write_text(
             json.dumps([asdict(r) for r in self.requests], indent=2) + "\n")
         self.log.event("ready", handoff=self.handoff, model_identity=self.engine.identity,

@@ -1393,11 +1393,13 @@ namespace hexkv {
 // share (36 MB, read from HBM: twenty caches per measurement, more than the
 // 256 MB MALL) 13.4-13.7 us at 320 positions against 14.1 at 384, 14.2 at
 // 352, 14.8 at 448, 15.5 at 512 and 16.1 at 256.  Above 64 MB,
-// 1024-position chunks, or 1280 from a million positions up (Llama-2-7B,
-// 0.34 M positions: 768, 1024 and equal pieces of 812 within 33.1-34.5 us
-// on HBM-resident data, 36.5 at 1280; Llama-3-8B, 2.0 M: 170.3-170.9 us at
-// 1280 against 173.0-173.2 at 1024, 179 for the grid and 179.6 at 512,
-// over three boxes).
+// 896-position chunks, or 1280 from a million positions up (Llama-2-7B,
+// 0.34 M positions, single-launch merge, HBM-resident, first and last
+// decode step: 30.2-31.7 us at 832-896 against 30.9-32.0 at 1024, 30.9-32.6
+// at 768, 32.6-33.4 at 1152, 32.0-34.0 at 640; with the second-launch merge
+// 896 had also led by 1-2%; Llama-3-8B, 2.0 M: 170.3-170.9 us at 1280
+// against 173.0-173.2 at 1024, 179 for the grid and 179.6 at 512, over
+// three boxes).
 //
 // Planned for the XCDs (split segments merged in the attention kernel, no
 // second launch), calls below 4 MB are split too, in pieces of about a
@@ -1411,7 +1413,7 @@ static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest, boo
     return static_cast<int>(std::max<int64_t>(64, (longest / 12 + 63) / 64 * 64));
   if (bytes < (INT64_C(4) << 20)) return static_cast<int>(std::max<int64_t>(64, (longest + 63) / 64 * 64));
   if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 240 + 63) / 64 * 64)));
-  return positions >= (INT64_C(1) << 20) ? 1280 : 1024;
+  return positions >= (INT64_C(1) << 20) ? 1280 : 896;
 }
 
 // Checks a planning request and returns the chunk hexkv_attend_plan cuts

@@ -310,12 +310,15 @@ int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_w
 
 /*
  * The chunk (positions per work item) hexkv_attend_plan uses for these
- * lengths: p->partition when set, else the library's choice -- one chunk per
- * segment below 4 MB read, about 240 items below 64 MB, 1024 positions
- * above (1280 from 2^20 positions up).  A caller that replays one captured
- * launch over several steps plans every step with the chunk of its last
- * (longest) step, passed as p->partition, so the item and partition counts
- * only grow and the last step's sizes bound every step.  Returns HEXKV_OK
+ * lengths: p->partition when set, else the library's choice -- below 4 MB
+ * read one chunk per segment (or, with work_xcds > 0, about a twelfth of the
+ * longest row, 64 positions at least), about 240 items below 64 MB, 896
+ * positions above (1280 from 2^20 positions up).  A caller that replays one
+ * captured launch over several steps can plan every step with the chunk of
+ * its last (longest) step, passed as p->partition, so the item and
+ * partition counts only grow and the last step's sizes bound every step
+ * (without work_xcds; planned for the XCDs, a list's length is the longest
+ * XCD share times the XCD count, which need not grow).  Returns HEXKV_OK
  * with *chunk set, or an error as hexkv_attend_plan.  No counterpart in the
  * reference (it has no planning step).
  */

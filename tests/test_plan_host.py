@@ -164,10 +164,10 @@ def test_plan_chunk_regimes():
     lens = [538 + 37 * i for i in range(32)]
     arr, _, mp = plan(params(32, 8, 1, 128), lens)
     assert 150 <= len(arr) <= 300 and mp > 1
-    # bandwidth-bound: 1024-position chunks, 1280 from a million positions up
+    # bandwidth-bound: 896-position chunks, 1280 from a million positions up
     lens = [2000 - 10 * i for i in range(64)]
     arr, _, _ = plan(params(64, 32, 8, 128), lens)
-    assert arr[:, 5].max() == 1024
+    assert arr[:, 5].max() == 896
     lens = [8000 - 100 * i for i in range(64)]
     arr, _, _ = plan(params(64, 32, 8, 128), lens)
     assert arr[:, 5].max() == 1280

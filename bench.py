@@ -489,19 +489,23 @@ def measure(w, device, args, steps, warmup, cpu_budget):
         job.run_graph()
     torch.cuda.synchronize()
     log(f"{w.name}: warmup done")
+    # The timed passes are enqueued back to back between two synchronisations
+    # (a synchronisation after every pass left the GPU idle before each pack,
+    # and the first milliseconds after idling ran 3-7% slow); each pass's
+    # events are read afterwards.
     pu_times, pack_times, decode_ms = [], [], []
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(n_ev)] for _ in range(steps)]
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for k in range(steps):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-        job.run_graph(ev)
-        torch.cuda.synchronize()
+        job.run_graph(events[k])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+    for k, ev in enumerate(events):
         pack_times.append(ev[0].elapsed_time(ev[1]))
         pu_times.append(ev[0].elapsed_time(ev[2]))
         decode_ms.append(ev[2].elapsed_time(ev[3]))
         log(f"{w.name} step {k}: pack+unpack {pu_times[-1]:.3f} ms, decode {decode_ms[-1]:.1f} ms")
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
 
     pu_ms = statistics.median(pu_times)
     pu_gbs = w.pack_unpack_bytes() / (pu_ms * 1e-3) / 1e9

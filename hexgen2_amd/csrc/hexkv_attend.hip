@@ -217,25 +217,44 @@ __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
 // with more to combine_kernel): one wave holds a head's (max, sum) pairs.
 constexpr int kMergeMaxParts = 64;  // also keeps each XCD's 8-bit arrival count from overflowing
 
+// Four consecutive outputs at p, one vector store when p is aligned for it
+// (output rows may have any element stride).
+template <typename T>
+__device__ __forceinline__ void store4(T *p, f32x4 v) {
+  if ((reinterpret_cast<uintptr_t>(p) & (4 * sizeof(T) - 1)) == 0) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<t4 *>(p) = t4{Elem<T>::from_float(v[0]), Elem<T>::from_float(v[1]),
+                                    Elem<T>::from_float(v[2]), Elem<T>::from_float(v[3])};
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p[k] = Elem<T>::from_float(v[k]);
+  }
+}
+
 // The XCD-local merge of a split segment (row, head group qh0 / G), after
 // this workgroup stored its partial: count the arrival; the last of the
 // segment's w.nparts items reads every partial from the XCD's L2 and writes
 // the normalised output, parts in index order (the result does not depend
-// on which item arrives last).  The partial loads of the first kDepth parts
-// go out together with the (max, sum) loads, so the merge waits for about
-// one L2 round trip: each thread owns VPT consecutive outputs of the G x D
-// block (one VPT-float load per part), and the waves turn the (max, sum)
-// pairs into per-part weights in LDS meanwhile.
+// on which item arrives last).
+//
+// Each thread owns 4 consecutive outputs of the G x D block, so the D / 4
+// lanes of a head sit in one wave.  Every lane loads its 4 outputs of each
+// part (one 16-byte load per part, parts past w.nparts not issued) and lane
+// k of a head the (max, sum) pairs of parts k, k + D / 4, ...; the head's
+// lanes then reduce the pairs into the part weights
+// w_p = 2^(m_p - max m) / sum_q 2^(m_q - max m) l_q, exchange them through
+// LDS within the wave, and accumulate.  One L2 round trip, no barrier after
+// the arrival, and one load instruction per wave and part.
 template <typename T, int D, int G>
 __device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w) {
   constexpr int OUT = G * D;
-  static_assert(OUT <= 4 * kAttThreads, "one pass over the segment's outputs");
-  constexpr int VPT = OUT >= 4 * kAttThreads ? 4 : OUT >= 2 * kAttThreads ? 2 : 1;
+  constexpr int LPH = D / 4;  // lanes per head
+  constexpr int R = (kMergeMaxParts + LPH - 1) / LPH;  // (max, sum) pairs per lane
   constexpr int kDepth = 16;
-  typedef float vecf __attribute__((ext_vector_type(VPT)));
+  static_assert(OUT <= 4 * kAttThreads && LPH <= 64, "one pass over the segment's outputs");
+  static_assert(kMergeMaxParts % kDepth == 0, "weight blocks stay inside s_w");
   __shared__ int s_last;
-  __shared__ float2 s_ml[G][kMergeMaxParts];
-  __shared__ float s_w[G][kMergeMaxParts];
+  __shared__ __attribute__((aligned(16))) float s_w[G][kMergeMaxParts];
   // Every wave's partial stores have reached the L2 before the arrival counts.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -251,84 +270,91 @@ __device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w) 
     if (s_last && old + mine != static_cast<uint64_t>(w.nparts) << (8 * x))
       raise_status(a.status, HEXKV_STATUS_PLACEMENT);
     if (static_cast<unsigned>(x) % a.n_xcd != blockIdx.x % a.n_xcd) raise_status(a.status, HEXKV_STATUS_DISPATCH);
+    if (s_last) __hip_atomic_store(count, static_cast<uint64_t>(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!s_last) return;
   // Drop this CU's L1 lines so the partials come from the L2.
   asm volatile("buffer_inv sc0" ::: "memory");
-  const int n = w.nparts, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t slot0 = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0) * a.max_parts;
-  const int i0 = tid * VPT;  // first output of this thread, (g, d) = (i0 / D, i0 % D)
-  const bool owner = i0 < OUT;
-  const int g = owner ? i0 / D : 0, d = i0 - g * D;
-  const float *o = a.ws_o + (slot0 + static_cast<int64_t>(g) * a.max_parts) * D + d;
-  vecf ov[kDepth];
+  const int n = w.nparts, tid = threadIdx.x, i0 = 4 * tid;
+  if (i0 >= OUT) return;
+  const int g = i0 / D, d = i0 - g * D, k = d / 4;
+  const int64_t slot = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0 + g) * a.max_parts;
+  const float *o = a.ws_o + slot * D + d;
+  const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml + slot * 2);
+  // The partials first: the pairs' loads then wait for nothing else.
+  f32x4 ov[kDepth];
 #pragma unroll
   for (int u = 0; u < kDepth; ++u)
-    ov[u] = owner && u < n ? *reinterpret_cast<const vecf *>(o + static_cast<int64_t>(u) * D) : vecf{};
-  for (int j = tid; j < G * n; j += kAttThreads) {
-    const int jg = j / n, jp = j - jg * n;
-    s_ml[jg][jp] = *reinterpret_cast<const float2 *>(a.ws_ml + (slot0 + static_cast<int64_t>(jg) * a.max_parts + jp) * 2);
-  }
-  __syncthreads();
-  // weights w_p = 2^(m_p - max m) / sum_p 2^(m_p - max m) l_p, one head per wave
-  for (int h = wave; h < G; h += kAttWaves) {
-    const float2 ml = lane < n ? s_ml[h][lane] : float2{kNoScore, 0.f};
-    const float mx = wave_max(ml.x);
-    const float e = lane < n ? fast_exp2(ml.x - mx) : 0.f;
-    const float total = sum_from<1>(e * ml.y);
-    if (lane < n) s_w[h][lane] = e / total;
-  }
-  __syncthreads();
-  if (!owner) return;
-  vecf acc{};
+    if (u < n) ov[u] = *reinterpret_cast<const f32x4 *>(o + static_cast<int64_t>(u) * D);
+  float2 mlv[R];
 #pragma unroll
-  for (int u = 0; u < kDepth; ++u)
-    if (u < n) acc += s_w[g][u] * ov[u];
-  for (int p0 = kDepth; p0 < n; p0 += kDepth) {
+  for (int j = 0; j < R; ++j) {
+    const int p = k + j * LPH;
+    mlv[j] = p < n ? ml[p] : float2{kNoScore, 0.f};
+  }
+  float mx = kNoScore;
+#pragma unroll
+  for (int j = 0; j < R; ++j) mx = fmaxf(mx, mlv[j].x);
+  mx = group_max<LPH>(mx);
+  float e[R], den = 0.f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    e[j] = fast_exp2(mlv[j].x - mx);
+    den = fmaf(e[j], mlv[j].y, den);
+  }
+  const float inv = 1.f / group_sum<LPH>(den);
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (k + j * LPH < n) s_w[g][k + j * LPH] = e[j] * inv;
+  __builtin_amdgcn_wave_barrier();  // the weights come from lanes of this wave
+  f32x4 acc{};
+  for (int p0 = 0; p0 < n; p0 += kDepth) {
+    if (p0 > 0) {
+#pragma unroll
+      for (int u = 0; u < kDepth; ++u)
+        if (p0 + u < n) ov[u] = *reinterpret_cast<const f32x4 *>(o + static_cast<int64_t>(p0 + u) * D);
+    }
+    f32x4 wq[kDepth / 4];  // weights of parts p0.. (p0 + kDepth <= kMergeMaxParts)
+#pragma unroll
+    for (int q = 0; q < kDepth / 4; ++q) wq[q] = *reinterpret_cast<const f32x4 *>(&s_w[g][p0 + 4 * q]);
 #pragma unroll
     for (int u = 0; u < kDepth; ++u)
-      ov[u] = p0 + u < n ? *reinterpret_cast<const vecf *>(o + static_cast<int64_t>(p0 + u) * D) : vecf{};
-#pragma unroll
-    for (int u = 0; u < kDepth; ++u)
-      if (p0 + u < n) acc += s_w[g][p0 + u] * ov[u];
+      if (p0 + u < n) acc += wq[u / 4][u % 4] * ov[u];
   }
-  T *out = static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D + i0;
-#pragma unroll
-  for (int v = 0; v < VPT; ++v) out[v] = Elem<T>::from_float(acc[v]);
-  if (tid == 0) __hip_atomic_store(count, static_cast<uint64_t>(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  store4(static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D + i0, acc);
 }
 
 // Merges the 4 waves' (max, sum, o) held in LDS into this partition's result:
 // the normalised output for a single-partition row, else a workspace partial
-// (merged here, XCD-locally, when the call has arrival counters).
+// (merged here, XCD-locally, when the call has arrival counters).  Each
+// thread takes 4 consecutive outputs of a head per pass (D is a multiple of
+// 16): one 16-byte LDS read per wave and one set of wave weights per pass.
 template <typename T, int D, int G>
 __device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
                                             const float (*s_acc)[G][D], const float (*s_m)[G],
                                             const float (*s_l)[G]) {
   T *out_row = static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D;
   const int64_t slot0 = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0) * a.max_parts;
-  for (int i = threadIdx.x; i < G * D; i += kAttThreads) {
+  for (int i = 4 * threadIdx.x; i < G * D; i += 4 * kAttThreads) {
     const int g = i / D, d = i - g * D;
     float mx = s_m[0][g];
 #pragma unroll
     for (int ww = 1; ww < kAttWaves; ++ww) mx = fmaxf(mx, s_m[ww][g]);
-    float o = 0.f, sum = 0.f;
+    f32x4 o{};
+    float sum = 0.f;
 #pragma unroll
     for (int ww = 0; ww < kAttWaves; ++ww) {
       const float c = fast_exp2(s_m[ww][g] - mx);
-      o = fmaf(c, s_acc[ww][g][d], o);
+      o += c * *reinterpret_cast<const f32x4 *>(&s_acc[ww][g][d]);
       sum = fmaf(c, s_l[ww][g], sum);
     }
     if (w.nparts == 1) {
-      out_row[i] = Elem<T>::from_float(o / sum);
+      store4(out_row + i, o * (1.f / sum));
     } else {
       const int64_t slot = slot0 + static_cast<int64_t>(g) * a.max_parts + w.part;
-      a.ws_o[slot * D + d] = o;
-      if (d == 0) {
-        a.ws_ml[slot * 2] = mx;
-        a.ws_ml[slot * 2 + 1] = sum;
-      }
+      *reinterpret_cast<f32x4 *>(a.ws_o + slot * D + d) = o;
+      if (d == 0) *reinterpret_cast<float2 *>(a.ws_ml + slot * 2) = float2{mx, sum};
     }
   }
   if (w.clamped && threadIdx.x == 0) raise_status(a.status, HEXKV_STATUS_LENGTH_CLAMPED);
@@ -437,7 +463,7 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   using L = Lanes<T, D>;
   constexpr int VEC = L::VEC, NV = L::NV, EPL = L::EPL, LPP = L::LPP, GPW = L::GPW, NG = L::NG;
   constexpr int STEP = NG * U;  // positions per workgroup iteration
-  __shared__ float s_acc[kAttWaves][G][D];
+  __shared__ __attribute__((aligned(16))) float s_acc[kAttWaves][G][D];
   __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
   __shared__ float s_kn[FT ? D : 1];
   // FT: two staged K tiles, STEP positions of D / VEC 16-byte chunks each,
@@ -849,7 +875,7 @@ __global__ __launch_bounds__(kAttThreads, 3) void attend_mfma_kernel(const Atten
   constexpr int PITCH = 2 * D + 32;  // LDS bytes per staged V row (padded: transposed reads spread over banks)
   static_assert(NJ >= 1 && VLPP <= 64 && UV >= 1 && UV * VPPI == 16, "head_dim");
   __shared__ __attribute__((aligned(16))) char s_v[kAttWaves][16 * PITCH];
-  __shared__ float s_acc[kAttWaves][G][D];
+  __shared__ __attribute__((aligned(16))) float s_acc[kAttWaves][G][D];
   __shared__ float s_m[kAttWaves][G], s_l[kAttWaves][G];
   Work w;
   if (!begin_work<T, D, G>(a, w)) return;

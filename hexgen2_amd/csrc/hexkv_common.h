@@ -147,6 +147,15 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Maximum over aligned groups of `LPP` consecutive lanes; every lane of a
+// group ends with the group's maximum.
+template <int LPP, int OFF = 1>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(LPP >= 1 && LPP <= 64 && (LPP & (LPP - 1)) == 0, "LPP must be a power of two");
+  if constexpr (OFF < LPP) return group_max<LPP, OFF * 2>(xor_step<OFF>(v, MaxOp{}));
+  else return v;
+}
+
 // Total (sum or max) over every offset in [FROM, 64): over the lanes that
 // agree in their low log2(FROM) bits.
 template <int FROM, typename Op>

@@ -499,6 +499,8 @@ def measure(w, device, args, steps, warmup, cpu_budget):
     t_start = time.perf_counter()
     for k in range(steps):
         job.run_graph(events[k])
+        if args.sync_passes:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t_start
     for k, ev in enumerate(events):
@@ -594,6 +596,9 @@ def main():
                     help="work lists whose split rows a second kernel merges (not planned for the XCDs)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the short dispatch sequence for hardware-counter runs")
+    ap.add_argument("--sync-passes", action="store_true",
+                    help="synchronise after every timed pass (for kernel traces: rocprofv3 faulted in one of "
+                         "its own threads with thousands of graph launches outstanding)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the KV path here runs prefill and decode on one "

@@ -273,6 +273,37 @@ def test_work_list_ragged_within_tolerance(device, hq, hkv, d, dtype, kernel):
     check(out[1:], q[1:], cache[1:], lens[1:], dtype)
 
 
+@pytest.mark.parametrize("hq,hkv,d,dtype,kernel", [(32, 4, 64, torch.float16, "mfma"),
+                                                   (32, 32, 128, torch.float16, "valu"),
+                                                   (8, 1, 128, torch.bfloat16, "mfma"),
+                                                   (4, 4, 16, torch.float32, "valu")])
+def test_output_at_odd_element_offset(device, hq, hkv, d, dtype, kernel):
+    """Output rows one element past a 16-byte boundary (a view into a larger
+    buffer): the kernels store four outputs at once only where the address
+    allows it, element by element otherwise.  The values must equal those
+    written to an aligned output bit for bit -- on the grid, on a work list
+    merged inside the attention kernel and on one merged by a second launch
+    -- and the element before the view stays untouched."""
+    lens = [0, 5, 64, 700, 2047]
+    q, cache = make(len(lens), 2112, hq, hkv, d, dtype, 17, device)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    for mode in ("grid", "list", "two-launch"):
+        print(f"odd output offset {kernel} hq={hq} hkv={hkv} d={d} {dtype} {mode}", flush=True)
+        kw = {} if mode == "grid" else dict(lens=lens, single_launch=mode == "list")
+        aligned = ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=64,
+                                       kernel=kernel, **kw)
+        buf = torch.full((q.numel() + 1,), 5.0, dtype=dtype, device=device)
+        odd = buf[1:].view(q.shape)
+        assert odd.data_ptr() % 16 != 0
+        ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, partition=64, kernel=kernel,
+                             out=odd, **kw)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(odd), bits(aligned))
+        assert buf[0].item() == 5.0
+        assert (aligned[0] == 0).all()
+        check(aligned[1:], q[1:], cache[1:], lens[1:], dtype)
+
+
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])
 def test_attend_plan_work_list_matches_grid_over_steps(device, kernel):
     # AttendPlan with host lengths (a list per step, shared by the layers)

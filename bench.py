@@ -36,7 +36,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from hexgen2_amd import ops  # noqa: E402
+from hexgen2_amd import _lib, ops  # noqa: E402
 from hexgen2_amd.workloads import WORKLOADS, workload  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
@@ -80,6 +80,12 @@ class Job:
             self.lists = ops.StepWorkLists(self.plan.params, w.lens, w.decode_steps, device, single_launch)
             self.plan.reserve(self.lists.lists)
         self.kernel_name = ops.attend_kernel(self.q[0], self.decode_layers[0], kernel)
+        if self.lists is not None:
+            # the kernel each step's list was planned with (the row-block kernel
+            # for "auto" on large calls)
+            names = {v: k for k, v in _lib.KERNELS.items()}
+            used = sorted({names[k] for k in self.lists.kernels})
+            self.kernel_name = "+".join(used)
         self.positions = self.seqlens.clone()
         self.graph = None
         # TinyLlama's 46 MB handoff fits in the 256 MB MALL: a 512 MB fill
@@ -93,9 +99,12 @@ class Job:
     def schedule(self):
         if self.grid:
             return "uniform grid, split rows merged by a second kernel"
+        rows = sum(k == _lib.KERNELS["rows"] for k in self.lists.kernels)
         return ("work lists planned per step up front (hexkv_attend_plan)"
                 + (f", for {self.lists.xcds} XCDs: split rows merged in the attention kernel (one launch)"
-                   if self.lists.xcds else ", split rows merged by a second kernel"))
+                   if self.lists.xcds else ", split rows merged by a second kernel")
+                + (f"; {rows} of {len(self.lists.kernels)} steps on the row-block kernel (items over "
+                   "adjacent KV heads of every cache row)" if rows else ""))
 
     def capture_graph(self):
         """The all-layer decode step as captured HIP graphs (after an eager

@@ -11,7 +11,7 @@ from pathlib import Path
 LIBRARY = Path(__file__).resolve().parent / "libhexkv.so"
 
 HEXKV_F16, HEXKV_BF16, HEXKV_F32 = 0, 1, 2
-KERNELS = {"auto": 0, "valu": 1, "mfma": 2}
+KERNELS = {"auto": 0, "valu": 1, "mfma": 2, "rows": 3}
 HEXKV_OK = 0
 HEXKV_EINVAL, HEXKV_ERANGE, HEXKV_EHIP, HEXKV_EUNSUPPORTED, HEXKV_EWORKSPACE = -1, -2, -3, -4, -5
 MAX_LAYERS_PER_LAUNCH = 96
@@ -22,15 +22,15 @@ EXPORTS = ("hexkv_version", "hexkv_last_error", "hexkv_pack", "hexkv_unpack", "h
            "hexkv_attend_workspace_bytes", "hexkv_attend_kernel", "hexkv_attend", "hexkv_flat_concat", "hexkv_batch_pad",
            "hexkv_head_concat", "hexkv_ipc_export", "hexkv_ipc_open", "hexkv_ipc_close",
            "hexkv_ipc_dlpack", "hexkv_ft_store", "hexkv_ft_attend_workspace_bytes", "hexkv_ft_attend",
-           "hexkv_attend_noalloc", "hexkv_attend_plan", "hexkv_attend_plan_chunk", "hexkv_device_status",
-           "hexkv_device_xcds")
+           "hexkv_attend_noalloc", "hexkv_attend_plan", "hexkv_attend_plan_chunk", "hexkv_attend_plan_kernel",
+           "hexkv_device_status", "hexkv_device_xcds")
 NOALLOC_SCRATCH_BYTES = 32 << 20
 # Arrival counters at the front of every attention workspace (zero them once).
 ATTEND_COUNTER_BYTES = 256 << 10
 ATTEND_COUNTER_WORDS = ATTEND_COUNTER_BYTES // 8  # one 64-bit counter per (row, head group)
 # Device status flags (hexkv_device_status).
-STATUS_APPEND_SKIPPED, STATUS_LENGTH_CLAMPED, STATUS_PLACEMENT, STATUS_DISPATCH = 1, 2, 4, 8
-STATUS_ERRORS = STATUS_APPEND_SKIPPED | STATUS_LENGTH_CLAMPED | STATUS_PLACEMENT
+STATUS_APPEND_SKIPPED, STATUS_LENGTH_CLAMPED, STATUS_PLACEMENT, STATUS_DISPATCH, STATUS_LIST = 1, 2, 4, 8, 16
+STATUS_ERRORS = STATUS_APPEND_SKIPPED | STATUS_LENGTH_CLAMPED | STATUS_PLACEMENT | STATUS_LIST
 
 
 class AttendParams(ctypes.Structure):
@@ -56,7 +56,7 @@ class WorkItem(ctypes.Structure):
     """Mirror of ``hexkv_work_item`` (32 bytes)."""
     _fields_ = [("row", ctypes.c_int32), ("head_group", ctypes.c_int32), ("part", ctypes.c_int32),
                 ("parts", ctypes.c_int32), ("first", ctypes.c_int32), ("count", ctypes.c_int32),
-                ("len", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("len", ctypes.c_int32), ("heads", ctypes.c_int32)]
 
 
 class FtAttendParams(ctypes.Structure):
@@ -129,6 +129,8 @@ def load() -> ctypes.CDLL:
                                       i32p, i32p]
     lib.hexkv_attend_plan_chunk.restype = ci
     lib.hexkv_attend_plan_chunk.argtypes = [ctypes.POINTER(AttendParams), vp, i32p]
+    lib.hexkv_attend_plan_kernel.restype = ci
+    lib.hexkv_attend_plan_kernel.argtypes = [ctypes.POINTER(AttendParams), vp, i32p]
     lib.hexkv_attend_noalloc.restype = ci
     lib.hexkv_attend_noalloc.argtypes = [ctypes.POINTER(AttendParams), vp]
     blocks = ctypes.POINTER(Block)

@@ -164,8 +164,14 @@ __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
   if (a.items) {
     const hexkv_work_item it = a.items[blockIdx.x];
     // Items come from device memory: one naming a row, head group, partition
-    // or positions outside this call's geometry does nothing.
+    // or positions outside this call's geometry does nothing; one planned
+    // for head groups of another size (another kernel) does nothing either,
+    // and says so.
     if (!work_item_fits(it, a.rows, a.n_groups, a.max_parts, a.max_seqlen)) return false;
+    if (it.heads != 0 && it.heads != G) {
+      if (threadIdx.x == 0) raise_status(a.status, HEXKV_STATUS_LIST);
+      return false;
+    }
     // The item holding a row's last position of head group 0 records the
     // row's new length (work lists read no seqlens, so this may alias them).
     if (a.lengths_out && threadIdx.x == 0 && it.head_group == 0 && it.len > 0 && it.count == it.len - it.first)
@@ -237,24 +243,24 @@ __device__ __forceinline__ void store4(T *p, f32x4 v) {
 // the normalised output, parts in index order (the result does not depend
 // on which item arrives last).
 //
-// Each thread owns 4 consecutive outputs of the G x D block, so the D / 4
-// lanes of a head sit in one wave.  Every lane loads its 4 outputs of each
-// part (one 16-byte load per part, parts past w.nparts not issued) and lane
-// k of a head the (max, sum) pairs of parts k, k + D / 4, ...; the head's
-// lanes then reduce the pairs into the part weights
-// w_p = 2^(m_p - max m) / sum_q 2^(m_q - max m) l_q, exchange them through
-// LDS within the wave, and accumulate.  One L2 round trip, no barrier after
-// the arrival, and one load instruction per wave and part.
+// Each thread owns 4 consecutive outputs of the G x D block per pass (1024
+// outputs a pass), so the D / 4 lanes of a head sit in one wave.  Every lane
+// loads its 4 outputs of each part (one 16-byte load per part, parts past
+// w.nparts not issued) and lane k of a head the (max, sum) pairs of parts k,
+// k + D / 4, ...; the head's lanes then reduce the pairs into the part
+// weights w_p = 2^(m_p - max m) / sum_q 2^(m_q - max m) l_q, exchange them
+// through LDS (s_w, G x kMergeMaxParts floats) within the wave, and
+// accumulate.  One L2 round trip per pass, no barrier after the arrival,
+// and one load instruction per wave and part.
 template <typename T, int D, int G>
-__device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w) {
+__device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w, float (*s_w)[kMergeMaxParts]) {
   constexpr int OUT = G * D;
   constexpr int LPH = D / 4;  // lanes per head
   constexpr int R = (kMergeMaxParts + LPH - 1) / LPH;  // (max, sum) pairs per lane
   constexpr int kDepth = 16;
-  static_assert(OUT <= 4 * kAttThreads && LPH <= 64, "one pass over the segment's outputs");
+  static_assert(D % 16 == 0 && LPH <= 64, "a head's outputs lie in one wave");
   static_assert(kMergeMaxParts % kDepth == 0, "weight blocks stay inside s_w");
   __shared__ int s_last;
-  __shared__ __attribute__((aligned(16))) float s_w[G][kMergeMaxParts];
   // Every wave's partial stores have reached the L2 before the arrival counts.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -276,61 +282,65 @@ __device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w) 
   if (!s_last) return;
   // Drop this CU's L1 lines so the partials come from the L2.
   asm volatile("buffer_inv sc0" ::: "memory");
-  const int n = w.nparts, tid = threadIdx.x, i0 = 4 * tid;
-  if (i0 >= OUT) return;
-  const int g = i0 / D, d = i0 - g * D, k = d / 4;
-  const int64_t slot = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0 + g) * a.max_parts;
-  const float *o = a.ws_o + slot * D + d;
-  const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml + slot * 2);
-  // The partials first: the pairs' loads then wait for nothing else.
-  f32x4 ov[kDepth];
-#pragma unroll
-  for (int u = 0; u < kDepth; ++u)
-    if (u < n) ov[u] = *reinterpret_cast<const f32x4 *>(o + static_cast<int64_t>(u) * D);
-  float2 mlv[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const int p = k + j * LPH;
-    mlv[j] = p < n ? ml[p] : float2{kNoScore, 0.f};
-  }
-  float mx = kNoScore;
-#pragma unroll
-  for (int j = 0; j < R; ++j) mx = fmaxf(mx, mlv[j].x);
-  mx = group_max<LPH>(mx);
-  float e[R], den = 0.f;
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    e[j] = fast_exp2(mlv[j].x - mx);
-    den = fmaf(e[j], mlv[j].y, den);
-  }
-  const float inv = 1.f / group_sum<LPH>(den);
-#pragma unroll
-  for (int j = 0; j < R; ++j)
-    if (k + j * LPH < n) s_w[g][k + j * LPH] = e[j] * inv;
-  __builtin_amdgcn_wave_barrier();  // the weights come from lanes of this wave
-  f32x4 acc{};
-  for (int p0 = 0; p0 < n; p0 += kDepth) {
-    if (p0 > 0) {
-#pragma unroll
-      for (int u = 0; u < kDepth; ++u)
-        if (p0 + u < n) ov[u] = *reinterpret_cast<const f32x4 *>(o + static_cast<int64_t>(p0 + u) * D);
-    }
-    f32x4 wq[kDepth / 4];  // weights of parts p0.. (p0 + kDepth <= kMergeMaxParts)
-#pragma unroll
-    for (int q = 0; q < kDepth / 4; ++q) wq[q] = *reinterpret_cast<const f32x4 *>(&s_w[g][p0 + 4 * q]);
+  const int n = w.nparts;
+  for (int i0 = 4 * static_cast<int>(threadIdx.x); i0 < OUT; i0 += 4 * kAttThreads) {
+    const int g = i0 / D, d = i0 - g * D, k = d / 4;
+    const int64_t slot = (static_cast<int64_t>(w.row) * a.q_heads + w.qh0 + g) * a.max_parts;
+    const float *o = a.ws_o + slot * D + d;
+    const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml + slot * 2);
+    // The partials first: the pairs' loads then wait for nothing else.
+    f32x4 ov[kDepth];
 #pragma unroll
     for (int u = 0; u < kDepth; ++u)
-      if (p0 + u < n) acc += wq[u / 4][u % 4] * ov[u];
+      if (u < n) ov[u] = *reinterpret_cast<const f32x4 *>(o + static_cast<int64_t>(u) * D);
+    float2 mlv[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int p = k + j * LPH;
+      mlv[j] = p < n ? ml[p] : float2{kNoScore, 0.f};
+    }
+    float mx = kNoScore;
+#pragma unroll
+    for (int j = 0; j < R; ++j) mx = fmaxf(mx, mlv[j].x);
+    mx = group_max<LPH>(mx);
+    float e[R], den = 0.f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      e[j] = fast_exp2(mlv[j].x - mx);
+      den = fmaf(e[j], mlv[j].y, den);
+    }
+    const float inv = 1.f / group_sum<LPH>(den);
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      if (k + j * LPH < n) s_w[g][k + j * LPH] = e[j] * inv;
+    __builtin_amdgcn_wave_barrier();  // the weights come from lanes of this wave
+    f32x4 acc{};
+    for (int p0 = 0; p0 < n; p0 += kDepth) {
+      if (p0 > 0) {
+#pragma unroll
+        for (int u = 0; u < kDepth; ++u)
+          if (p0 + u < n) ov[u] = *reinterpret_cast<const f32x4 *>(o + static_cast<int64_t>(p0 + u) * D);
+      }
+      f32x4 wq[kDepth / 4];  // weights of parts p0.. (p0 + kDepth <= kMergeMaxParts)
+#pragma unroll
+      for (int q = 0; q < kDepth / 4; ++q) wq[q] = *reinterpret_cast<const f32x4 *>(&s_w[g][p0 + 4 * q]);
+#pragma unroll
+      for (int u = 0; u < kDepth; ++u)
+        if (p0 + u < n) acc += wq[u / 4][u % 4] * ov[u];
+    }
+    store4(static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D + i0, acc);
   }
-  store4(static_cast<T *>(a.out) + w.b * a.o_bs + w.t * a.o_rs + w.qh0 * D + i0, acc);
 }
 
-// Merges the 4 waves' (max, sum, o) held in LDS into this partition's result:
-// the normalised output for a single-partition row, else a workspace partial
-// (merged here, XCD-locally, when the call has arrival counters).  Each
-// thread takes 4 consecutive outputs of a head per pass (D is a multiple of
-// 16): one 16-byte LDS read per wave and one set of wave weights per pass.
-template <typename T, int D, int G>
+// Merges the NS slots' (max, sum, o) held in LDS (the 4 waves' of the
+// attention kernels, the position slots' of the row-block kernel) into this
+// partition's result: the normalised output for a single-partition row,
+// else a workspace partial (merged here, XCD-locally, when the call has
+// arrival counters).  Each thread takes 4 consecutive outputs of a head per
+// pass (D is a multiple of 16): one 16-byte LDS read per slot and one set of
+// slot weights per pass.  With W_IN_ACC the merge's weights reuse s_acc
+// (read completely before the merge's first barrier).
+template <typename T, int D, int G, int NS = kAttWaves, bool W_IN_ACC = false>
 __device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
                                             const float (*s_acc)[G][D], const float (*s_m)[G],
                                             const float (*s_l)[G]) {
@@ -340,11 +350,11 @@ __device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
     const int g = i / D, d = i - g * D;
     float mx = s_m[0][g];
 #pragma unroll
-    for (int ww = 1; ww < kAttWaves; ++ww) mx = fmaxf(mx, s_m[ww][g]);
+    for (int ww = 1; ww < NS; ++ww) mx = fmaxf(mx, s_m[ww][g]);
     f32x4 o{};
     float sum = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kAttWaves; ++ww) {
+    for (int ww = 0; ww < NS; ++ww) {
       const float c = fast_exp2(s_m[ww][g] - mx);
       o += c * *reinterpret_cast<const f32x4 *>(&s_acc[ww][g][d]);
       sum = fmaf(c, s_l[ww][g], sum);
@@ -358,8 +368,14 @@ __device__ __forceinline__ void finish_work(const AttendArgs &a, const Work &w,
     }
   }
   if (w.clamped && threadIdx.x == 0) raise_status(a.status, HEXKV_STATUS_LENGTH_CLAMPED);
-  if constexpr (G * D <= 4 * kAttThreads) {  // the host merges larger blocks with combine_kernel
-    if (w.nparts > 1 && a.seg_count) merge_split<T, D, G>(a, w);
+  if (w.nparts > 1 && a.seg_count) {
+    if constexpr (W_IN_ACC) {
+      static_assert(NS * D >= kMergeMaxParts, "the merge's weights fit in s_acc");
+      merge_split<T, D, G>(a, w, reinterpret_cast<float (*)[kMergeMaxParts]>(const_cast<float *>(&s_acc[0][0][0])));
+    } else if constexpr (G * D <= 4 * kAttThreads) {  // the host merges larger blocks with combine_kernel
+      __shared__ __attribute__((aligned(16))) float s_w[G][kMergeMaxParts];
+      merge_split<T, D, G>(a, w, s_w);
+    }
   }
 }
 
@@ -787,6 +803,217 @@ __global__ __launch_bounds__(kAttThreads) void attend_valu_kernel(const AttendAr
   }
   __syncthreads();
   finish_work<T, D, G>(a, w, s_acc, s_m, s_l);
+}
+
+// ------------------------------------------------------ row-block path ---
+//
+// attend_rows_kernel: a work item covers HB consecutive KV heads of one
+// row's positions [p0, p0 + n), with the GQ query heads of each, so the
+// workgroup reads whole cache rows (HB = the row's KV head count) instead of
+// one head's 2 D-element slices out of every row.  Measured on MI355X in a
+// read-only probe over 4 KB rows of 8 heads: one head per workgroup and XCD
+// 6.6-6.7 TB/s with the odd heads' slices served last (the XCDs reading
+// them finished ~55 us after the others in a ~320 us stream; each head
+// alone streams at the same rate as any other), whole rows per workgroup
+// 7.1 TB/s with the XCDs finishing within ~18 us.
+//
+// Lane group gid (LPP lanes, one D-element head slice) takes KV head
+// hh = gid % HB at position slot ps = gid / HB: NG / HB positions per load
+// slot, U slots per iteration.  Each lane keeps the running-softmax state of
+// its head's GQ query heads; the slots of a head are merged through LDS at
+// the end (finish_work over NG / HB slots), and a split segment
+// (row, head block) merges XCD-locally like the other kernels'.
+template <typename T, int D, int GQ, int HB, int U>
+__global__ __launch_bounds__(kAttThreads) void attend_rows_kernel(const AttendArgs a) {
+  using E = Elem<T>;
+  using L = Lanes<T, D>;
+  constexpr int VEC = L::VEC, NV = L::NV, EPL = L::EPL, LPP = L::LPP, GPW = L::GPW, NG = L::NG;
+  constexpr int PS = NG / HB, QH = HB * GQ, STEP = PS * U;
+  static_assert(NG % HB == 0, "the head block divides the lane groups");
+  __shared__ __attribute__((aligned(16))) float s_acc[PS][QH][D];
+  __shared__ float s_m[PS][QH], s_l[PS][QH];
+  Work w;
+  if (!begin_work<T, D, QH>(a, w)) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane % LPP, gid = wave * GPW + lane / LPP;
+  const int hh = gid % HB, ps = gid / HB;
+  const float scale = a.scale_log2;
+
+  u32x4 qv[GQ][NV];
+  {
+    const T *qrow = static_cast<const T *>(a.q) + w.b * a.q_bs + w.t * a.q_rs + (w.qh0 + hh * GQ) * D + sub * EPL;
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) qv[g][v] = *reinterpret_cast<const u32x4 *>(qrow + g * D + v * VEC);
+  }
+
+  // Uniform bases at the block's first KV head; each lane's 32-bit offset
+  // adds its head's slice within the row.
+  const char *kseq = static_cast<const char *>(a.cache) +
+                     (w.b * a.c_bs + static_cast<int64_t>(w.hk) * D) * static_cast<int64_t>(sizeof(T));
+  const char *vseq = kseq + a.c_kv * static_cast<int64_t>(sizeof(T));
+  const uint32_t row_bytes = static_cast<uint32_t>(a.c_ps * sizeof(T));
+  const uint32_t lane_off = static_cast<uint32_t>((hh * D + sub * EPL) * sizeof(T));
+  const uint32_t lane_base = static_cast<uint32_t>(w.p0 + ps) * row_bytes + lane_off;
+
+  float m[GQ], l[GQ], acc[GQ][EPL];
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+    m[g] = kNoScore;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+  }
+
+  // Slot u of the iteration at i0 holds position i0 + u * PS + ps; TAIL
+  // clamps positions past n_cache to the last cached one (finite data) and
+  // `consume` masks their scores.
+  using Slots = u32x4[U][NV];
+  auto fetch = [&](int i0, Slots &kr, Slots &vr, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t off;
+      if constexpr (TAIL) {
+        const int pp = min(i0 + u * PS + ps, w.n_cache - 1);
+        off = static_cast<uint32_t>(w.p0 + pp) * row_bytes + lane_off;
+      } else {
+        off = lane_base + static_cast<uint32_t>(i0 + u * PS) * row_bytes;
+      }
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        kr[u][v] = load16(kseq, off + v * 16);
+        vr[u][v] = load16(vseq, off + v * 16);
+      }
+    }
+  };
+  auto consume = [&](int i0, const Slots &kr, const Slots &vr, auto tail) {
+    constexpr bool TAIL = decltype(tail)::value;
+    float sc[U][GQ];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) {
+        float d = E::dot(qv[g][0], kr[u][0], 0.f);
+#pragma unroll
+        for (int v = 1; v < NV; ++v) d = E::dot(qv[g][v], kr[u][v], d);
+        sc[u][g] = group_sum<LPP>(d);
+      }
+    if constexpr (TAIL) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool valid = i0 + u * PS + ps < w.n_cache;
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) sc[u][g] = valid ? sc[u][g] : -INFINITY;
+      }
+    }
+    float mt[GQ];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      float x = sc[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) x = fmaxf(x, sc[u][g]);
+      mt[g] = x * scale;
+    }
+    lazy_rescale<GQ, EPL>(mt, m, l, acc);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vf[EPL];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) E::to_float(vr[u][v], vf + v * VEC);
+#pragma unroll
+      for (int g = 0; g < GQ; ++g) {
+        const float pr = fast_exp2(fmaf(sc[u][g], scale, -m[g]));
+        l[g] += pr;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
+      }
+    }
+  };
+
+  // Full iterations with the next one's loads in flight, then the tail.
+  const int n_full = w.n_cache / STEP * STEP;
+  int i0 = 0;
+  if (n_full > 0) {
+    Slots ka, va;
+    fetch(0, ka, va, std::false_type{});
+    for (; i0 + STEP < n_full; i0 += STEP) {
+      Slots kb, vb;
+      fetch(i0 + STEP, kb, vb, std::false_type{});
+      consume(i0, ka, va, std::false_type{});
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          ka[u][v] = kb[u][v];
+          va[u][v] = vb[u][v];
+        }
+    }
+    consume(i0, ka, va, std::false_type{});
+    i0 += STEP;
+  }
+  if (i0 < w.n_cache) {
+    Slots kr, vr;
+    fetch(i0, kr, vr, std::true_type{});
+    consume(i0, kr, vr, std::true_type{});
+  }
+
+  if (w.has_new) {
+    // The new row of every head of the block: attended by the lane groups of
+    // slot 0 from kv_new, written to the cache by them (one head each).
+    const char *knew = static_cast<const char *>(a.kv_new) +
+                       ((static_cast<int64_t>(w.b) * 2 * a.kv_heads + w.hk + hh) * D + sub * EPL) *
+                           static_cast<int64_t>(sizeof(T));
+    const char *vnew = knew + static_cast<int64_t>(a.kv_heads) * D * sizeof(T);
+    u32x4 kn[NV], vn[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      kn[v] = *reinterpret_cast<const u32x4 *>(knew + v * 16);
+      vn[v] = *reinterpret_cast<const u32x4 *>(vnew + v * 16);
+    }
+    float sc[GQ], mt[GQ];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      float d = E::dot(qv[g][0], kn[0], 0.f);
+#pragma unroll
+      for (int v = 1; v < NV; ++v) d = E::dot(qv[g][v], kn[v], d);
+      sc[g] = ps == 0 ? group_sum<LPP>(d) : -INFINITY;
+      mt[g] = sc[g] * scale;
+    }
+    lazy_rescale<GQ, EPL>(mt, m, l, acc);
+    float vf[EPL];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) E::to_float(vn[v], vf + v * VEC);
+#pragma unroll
+    for (int g = 0; g < GQ; ++g) {
+      const float pr = fast_exp2(fmaf(sc[g], scale, -m[g]));
+      l[g] += pr;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pr, vf[e], acc[g][e]);
+    }
+    if (w.writer && ps == 0) {
+      const uint32_t off = static_cast<uint32_t>(w.pos_new) * row_bytes + lane_off;
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(kseq) + off + v * 16) = kn[v];
+        *reinterpret_cast<u32x4 *>(const_cast<char *>(vseq) + off + v * 16) = vn[v];
+      }
+    }
+  }
+
+#pragma unroll
+  for (int g = 0; g < GQ; ++g) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s_acc[ps][hh * GQ + g][sub * EPL + e] = acc[g][e];
+    if (sub == 0) {
+      s_m[ps][hh * GQ + g] = m[g];
+      s_l[ps][hh * GQ + g] = l[g];
+    }
+  }
+  __syncthreads();
+  finish_work<T, D, QH, PS, true>(a, w, s_acc, s_m, s_l);
 }
 
 // ------------------------------------------------------------- MFMA path ---
@@ -1221,6 +1448,35 @@ static int kernel_group(int group) {
   return 1;
 }
 
+// KV heads per work item of the row-block kernel (HEXKV_KERNEL_ROWS), or 0
+// when these parameters do not fit it (16-bit data, head_dim 128, 2+ KV
+// heads, 1, 2 or 4 query heads per KV head).  2 for grouped queries, 8 (else
+// the largest of 4, 2 dividing the KV heads) for one query head per KV head:
+// measured per call at Llama-3-8B's shape (bf16, 8 KV heads, group 4;
+// decode steps 0 / 128 / 255, ~400 items) 152.3 / 158.9 / 163.2 us with 2
+// heads per item, 157.3 / 160.8 / 164.6 with 4 and 155.7 / 161.6 / 166.8
+// with 8, against 166.2 / 170.3 / 175.7 with one head per item; at
+// Llama-2-7B's (fp16, 32 KV heads, group 1; steps 0 / 32 / 63) 29.9 / 30.6 /
+// 31.3 with 8, 31.3 / 31.8 / 32.5 with 2 and 31.4 / 32.7 / 33.4 with 4,
+// against 31.2 / 32.1 / 32.5.
+static int rows_block(const hexkv_attend_params *p) {
+  if (p->dtype == HEXKV_F32 || p->head_dim != 128 || p->kv_heads < 2) return 0;
+  const int group = p->q_heads / p->kv_heads;
+  if (group != 1 && group != 2 && group != 4) return 0;
+  if (group > 1) return p->kv_heads % 2 == 0 ? 2 : 0;
+  for (int hb : {8, 4, 2})
+    if (p->kv_heads % hb == 0) return hb;
+  return 0;
+}
+
+// Query heads per (row, head group) segment: a head block's for the
+// row-block kernel, a kernel group's otherwise.
+static int segment_heads(const hexkv_attend_params *p) {
+  const int group = p->q_heads / p->kv_heads;
+  if (p->kernel == HEXKV_KERNEL_ROWS) return rows_block(p) * group;
+  return kernel_group(group);
+}
+
 // Partition size: about (rows x head groups x positions) / 2048 positions,
 // as a power of two in [128, 512], counting half of max_seqlen per row
 // (ragged batches average about that).  Measured on MI355X (attention +
@@ -1288,15 +1544,21 @@ static int validate(const hexkv_attend_params *p) {
                 p->max_seqlen, static_cast<long long>(p->capacity));
   // With a work list the items carry the positions and the partition is not
   // read; it may then hold the list's chunk, which can exceed 4096.
-  if (p->partition < 0 || (p->partition > 0 && p->partition % 64 != 0) ||
+  // (Row-block lists are cut in multiples of 16 positions.)
+  const int grain = p->kernel == HEXKV_KERNEL_ROWS ? 16 : 64;
+  if (p->partition < 0 || (p->partition > 0 && p->partition % grain != 0) ||
       (!p->work_items_dev && p->partition > 4096))
-    return fail(HEXKV_EINVAL, "hexkv_attend: partition must be 0 or a multiple of 64 (up to 4096 without a work list)");
+    return fail(HEXKV_EINVAL, "hexkv_attend: partition must be 0 or a multiple of %d (up to 4096 without a work list)",
+                grain);
   if (!(p->softmax_scale > 0.f) || p->softmax_scale > 3.0e38f)
     return fail(HEXKV_EINVAL, "hexkv_attend: softmax_scale must be positive and finite");
-  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_MFMA)
+  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_ROWS)
     return fail(HEXKV_EINVAL, "hexkv_attend: unknown kernel %d", p->kernel);
   if (p->kernel == HEXKV_KERNEL_MFMA && (p->dtype == HEXKV_F32 || p->head_dim < 64))
     return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the MFMA kernel takes float16/bfloat16 with head_dim >= 64");
+  if (p->kernel == HEXKV_KERNEL_ROWS && !rows_block(p))
+    return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the row-block kernel takes float16/bfloat16, head_dim 128, "
+                                    "2+ KV heads and 1, 2 or 4 query heads per KV head");
   if (p->work_xcds < 0 || p->work_xcds > 64) return fail(HEXKV_EINVAL, "hexkv_attend: work_xcds outside [0, 64]");
   if (p->lengths_out_dev && (!p->work_items_dev || !p->kv_new))
     return fail(HEXKV_EINVAL, "hexkv_attend: lengths_out_dev needs a work list and kv_new");
@@ -1309,12 +1571,17 @@ static int validate(const hexkv_attend_params *p) {
       return fail(HEXKV_EINVAL, "hexkv_attend: work_items_dev must be 16-byte aligned, work_parts_dev 4-byte");
     if (p->q_len != 1 || p->causal)
       return fail(HEXKV_EINVAL, "hexkv_attend: a work list is for decode rows (q_len 1, not causal)");
-    if (p->work_xcds > 0 &&
-        static_cast<int64_t>(p->batch) * (p->q_heads / kernel_group(p->q_heads / p->kv_heads)) > kCounterWords)
+    if (p->work_xcds > 0 && static_cast<int64_t>(p->batch) * (p->q_heads / segment_heads(p)) > kCounterWords)
       return fail(HEXKV_EINVAL, "hexkv_attend: the single-launch merge counts at most %lld (row, head group) "
                                 "segments; use work_xcds 0", static_cast<long long>(kCounterWords));
+    if (p->kernel == HEXKV_KERNEL_ROWS &&
+        (p->work_xcds < 1 || p->work_xcds > 8 || p->work_max_parts > kMergeMaxParts))
+      return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the row-block kernel merges in the kernel: a list planned "
+                                      "for 1-8 XCDs with at most %d partitions per segment", kMergeMaxParts);
   } else if (p->work_xcds > 0) {
     return fail(HEXKV_EINVAL, "hexkv_attend: work_xcds is for work lists");
+  } else if (p->kernel == HEXKV_KERNEL_ROWS) {
+    return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: the row-block kernel runs work lists only");
   }
   if (p->lengths_out_dev && (reinterpret_cast<uintptr_t>(p->lengths_out_dev) & 3u))
     return fail(HEXKV_EINVAL, "hexkv_attend: lengths_out_dev must be 4-byte aligned");
@@ -1376,6 +1643,31 @@ static void launch(const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
     constexpr int SL = kAttThreads / D >= 1 ? kAttThreads / D : 1;
     if (a.max_parts <= 8 * SL) combine_kernel<T, D, G, 8><<<cgrid, kAttThreads, 0, s>>>(a);
     else combine_kernel<T, D, G, 32><<<cgrid, kAttThreads, 0, s>>>(a);
+  }
+}
+
+// The row-block kernel (head_dim 128, 16-bit): GQ query heads per KV head,
+// HB KV heads per item.
+template <typename T, int GQ>
+static int dispatch_rows_hb(int HB, const AttendArgs &a, dim3 grid, hipStream_t s) {
+  constexpr int U = slots<T, 128, GQ>();
+  switch (HB) {
+    case 2: attend_rows_kernel<T, 128, GQ, 2, U><<<grid, kAttThreads, 0, s>>>(a); break;
+    case 4: attend_rows_kernel<T, 128, GQ, 4, U><<<grid, kAttThreads, 0, s>>>(a); break;
+    case 8: attend_rows_kernel<T, 128, GQ, 8, U><<<grid, kAttThreads, 0, s>>>(a); break;
+    case 16: attend_rows_kernel<T, 128, GQ, 16, U><<<grid, kAttThreads, 0, s>>>(a); break;
+    default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: head block %d", HB);
+  }
+  return HEXKV_OK;
+}
+
+template <typename T>
+static int dispatch_rows(int GQ, int HB, const AttendArgs &a, dim3 grid, hipStream_t s) {
+  switch (GQ) {
+    case 1: return dispatch_rows_hb<T, 1>(HB, a, grid, s);
+    case 2: return dispatch_rows_hb<T, 2>(HB, a, grid, s);
+    case 4: return dispatch_rows_hb<T, 4>(HB, a, grid, s);
+    default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: group %d", GQ);
   }
 }
 
@@ -1449,8 +1741,19 @@ static int plan_request(const hexkv_attend_params *p, const int32_t *lens, const
   if (p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads || p->batch < 0 || p->batch > 65535)
     return fail(HEXKV_EINVAL, "%s: bad batch or head counts", what);
   if (p->q_len != 1 || p->causal) return fail(HEXKV_EINVAL, "%s: work lists are for decode rows (q_len 1, not causal)", what);
-  if (p->partition < 0 || (p->partition > 0 && (p->partition % 64 != 0 || p->partition > (1 << 30))))
-    return fail(HEXKV_EINVAL, "%s: partition must be 0 or a positive multiple of 64", what);
+  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_ROWS)
+    return fail(HEXKV_EINVAL, "%s: unknown kernel %d", what, p->kernel);
+  // Row-block items hold several heads per position: finer chunks.
+  const int grain = p->kernel == HEXKV_KERNEL_ROWS ? 16 : 64;
+  if (p->partition < 0 || (p->partition > 0 && (p->partition % grain != 0 || p->partition > (1 << 30))))
+    return fail(HEXKV_EINVAL, "%s: partition must be 0 or a positive multiple of %d", what, grain);
+  const int hb = p->kernel == HEXKV_KERNEL_ROWS ? rows_block(p) : 1;
+  if (!hb || (p->kernel == HEXKV_KERNEL_ROWS && p->work_xcds < 1))
+    return fail(HEXKV_EUNSUPPORTED, "%s: the row-block kernel takes float16/bfloat16, head_dim 128, 2+ KV heads, "
+                                    "1, 2 or 4 query heads per KV head, and a list planned for the XCDs", what);
+  // Segment positions as the per-KV-head kernels count them (the chunk rule
+  // below is measured in those); a row-block item holds hb of them per
+  // position.
   const int groups = p->q_heads / kernel_group(p->q_heads / p->kv_heads);
   const int extra = p->kv_new ? 1 : 0;
   int64_t positions = 0, longest = 0;
@@ -1462,9 +1765,25 @@ static int plan_request(const hexkv_attend_params *p, const int32_t *lens, const
     positions += len * groups;
     longest = std::max(longest, len);
   }
-  if (p->partition > 0) return p->partition;
+  if (p->partition > 0) {
+    if (hb > 1 && (longest + p->partition - 1) / p->partition > kMergeMaxParts)
+      return fail(HEXKV_EUNSUPPORTED, "%s: partition %d cuts a %lld-key row into more than %d pieces, which the "
+                                      "row-block kernel cannot merge", what, p->partition,
+                  static_cast<long long>(longest), kMergeMaxParts);
+    return p->partition;
+  }
   const int64_t row_bytes = 2 * static_cast<int64_t>(p->head_dim) * elem_size(p->dtype);
-  return plan_chunk(positions, row_bytes, longest, p->work_xcds > 0);
+  if (hb == 1) return plan_chunk(positions, row_bytes, longest, p->work_xcds > 0);
+  // Row-block lists: about kRowsItems items (measured best at both shapes
+  // the kernel was tuned on: Llama-3-8B 152-164 us per call at ~400 items
+  // of 2 heads, 178-181 at ~200 and 153-164 at ~800; Llama-2-7B 29.9-31.3 at
+  // ~400 items of 8 heads, 41 at ~200), in multiples of 16 positions, with
+  // at most kMergeMaxParts pieces per row.
+  constexpr int64_t kRowsItems = 400;
+  const int64_t block_positions = positions / hb;  // positions x head blocks
+  const int64_t fewest = (longest + kMergeMaxParts - 1) / kMergeMaxParts;  // positions per piece
+  const int64_t c = std::max<int64_t>({16, (block_positions / kRowsItems + 15) / 16 * 16, (fewest + 15) / 16 * 16});
+  return static_cast<int>(c);
 }
 
 }  // namespace hexkv
@@ -1479,6 +1798,28 @@ extern "C" int hexkv_attend_plan_chunk(const hexkv_attend_params *p, const int32
   return HEXKV_OK;
 }
 
+extern "C" int hexkv_attend_plan_kernel(const hexkv_attend_params *p, const int32_t *lens, int32_t *kernel) {
+  using namespace hexkv;
+  clear_error();
+  if (!kernel) return fail(HEXKV_EINVAL, "hexkv_attend_plan_kernel: null argument");
+  const int c = plan_request(p, lens, "hexkv_attend_plan_kernel");
+  if (c < 0) return c;
+  if (p->kernel != HEXKV_KERNEL_AUTO) {
+    *kernel = p->kernel;
+    return HEXKV_OK;
+  }
+  *kernel = use_mfma(p, kernel_group(p->q_heads / p->kv_heads)) ? HEXKV_KERNEL_MFMA : HEXKV_KERNEL_VALU;
+  if (rows_block(p) && p->work_xcds >= 1 && p->work_xcds <= 8) {
+    // Bytes the call reads: every attended position of every KV head.
+    int64_t positions = 0;
+    const int extra = p->kv_new ? 1 : 0;
+    for (int b = 0; b < p->batch; ++b) positions += static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+    const int64_t bytes = positions * p->kv_heads * 2 * p->head_dim * elem_size(p->dtype);
+    if (bytes >= (INT64_C(64) << 20)) *kernel = HEXKV_KERNEL_ROWS;
+  }
+  return HEXKV_OK;
+}
+
 namespace hexkv {
 
 // The work list of a planning request, in launch order (see hexkv_attend_plan),
@@ -1486,7 +1827,7 @@ namespace hexkv {
 static int build_plan(const hexkv_attend_params *p, const int32_t *lens, int64_t chunk,
                       std::vector<hexkv_work_item> &out, std::vector<int32_t> &seg_parts, int32_t *max_parts,
                       const char *what) {
-  const int G = kernel_group(p->q_heads / p->kv_heads);
+  const int G = segment_heads(p);
   const int groups = p->q_heads / G;
   const int64_t segs = static_cast<int64_t>(p->batch) * groups;
   const int extra = p->kv_new ? 1 : 0;
@@ -1540,7 +1881,7 @@ static int build_plan(const hexkv_attend_params *p, const int32_t *lens, int64_t
     it.first = static_cast<int32_t>(first);
     it.count = static_cast<int32_t>(cnt);
     it.len = static_cast<int32_t>(len[b]);
-    it.reserved = 0;
+    it.heads = G;
     lists[home[static_cast<size_t>(b) * groups + hg]].push_back(it);
   };
   std::vector<std::pair<int64_t, int64_t>> tails;  // (positions, b * groups + hg)
@@ -1616,8 +1957,9 @@ extern "C" int hexkv_attend_kernel(const hexkv_attend_params *p) {
   clear_error();
   if (!p || p->q_heads < 1 || p->kv_heads < 1 || p->q_heads % p->kv_heads != 0)
     return fail(HEXKV_EINVAL, "hexkv_attend_kernel: bad q_heads/kv_heads");
-  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_MFMA)
+  if (p->kernel < HEXKV_KERNEL_AUTO || p->kernel > HEXKV_KERNEL_ROWS)
     return fail(HEXKV_EINVAL, "hexkv_attend_kernel: unknown kernel %d", p->kernel);
+  if (p->kernel == HEXKV_KERNEL_ROWS) return HEXKV_KERNEL_ROWS;
   return use_mfma(p, kernel_group(p->q_heads / p->kv_heads)) ? HEXKV_KERNEL_MFMA : HEXKV_KERNEL_VALU;
 }
 
@@ -1669,20 +2011,23 @@ static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t w
     a.ws_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + HEXKV_ATTEND_COUNTER_BYTES);
     a.ws_ml = a.ws_o + rows * p->q_heads * max_parts * p->head_dim;
   }
-  a.n_groups = p->q_heads / G;
+  const bool rows_kernel = p->kernel == HEXKV_KERNEL_ROWS;
+  a.n_groups = p->q_heads / segment_heads(p);
   a.rows = static_cast<int32_t>(rows);
   a.items = p->work_items_dev;
   a.seg_parts = p->work_parts_dev;
   // Split segments of a list planned for the XCDs merge in the attention
-  // kernel, counting arrivals in the workspace's counter words.
+  // kernel, counting arrivals in the workspace's counter words (the
+  // row-block kernel's always: validate() holds it to such lists).
   a.seg_count = (a.items && p->work_xcds > 0 && p->work_xcds <= 8 && need > 0 && max_parts <= kMergeMaxParts &&
-                 G * p->head_dim <= 4 * kAttThreads)
+                 (rows_kernel || G * p->head_dim <= 4 * kAttThreads))
                     ? static_cast<uint64_t *>(workspace) : nullptr;
   a.n_xcd = p->work_xcds;
   a.lengths_out = p->lengths_out_dev;
   // The status word, where a kernel may raise a flag: lengths read from
-  // seqlens (clamped), XCD placement of a single-launch merge.
-  if (((a.seqlens && !a.items) || a.seg_count) && (rc = status_word(stream, &a.status, what)) != HEXKV_OK)
+  // seqlens (clamped), XCD placement of a single-launch merge, work items
+  // planned for another kernel.
+  if ((a.seqlens || a.items) && (rc = status_word(stream, &a.status, what)) != HEXKV_OK)
     return rc;
 
   dim3 grid;
@@ -1698,6 +2043,12 @@ static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t w
     grid = dim3(grid_x, static_cast<unsigned>(p->q_heads / G), static_cast<unsigned>(rows));
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rows_kernel) {
+    const int GQ = p->q_heads / p->kv_heads, HB = rows_block(p);
+    rc = p->dtype == HEXKV_BF16 ? dispatch_rows<__bf16>(GQ, HB, a, grid, s) : dispatch_rows<_Float16>(GQ, HB, a, grid, s);
+    if (rc != HEXKV_OK) return rc;
+    return check_launch(what);
+  }
   const int kind = use_mfma(p, G) ? kLaunchMfma : kLaunchValu;
   switch (p->dtype) {
     case HEXKV_BF16: rc = dispatch_d<__bf16>(p->head_dim, G, a, grid, kind, s); break;

@@ -64,6 +64,8 @@ _STATUS_TEXT = {
                                 "append, its own new key)",
     _lib.STATUS_PLACEMENT: "the work items of a split segment ran on more than one XCD, so that segment's "
                            "single-launch merge may have read stale partials",
+    _lib.STATUS_LIST: "a work list planned for another attention kernel (another head-group size) was "
+                      "launched, and its items were skipped",
 }
 
 
@@ -409,15 +411,19 @@ class WorkList:
     """A ``hexkv_attend_plan`` work list in device memory: ``items``
     (``[n_items, 8]`` int32, one ``hexkv_work_item`` per workgroup) and
     ``parts`` (partitions per (row, head group)), valid for the lengths and
-    ``seqlen_bias``/``max_seqlen`` it was built for."""
+    ``seqlen_bias``/``max_seqlen`` it was built for.  ``kernel`` is the
+    ``hexkv_attend_params.kernel`` value it was planned with (the row-block
+    kernel plans other head groups), which launches of the list use."""
 
-    def __init__(self, items: torch.Tensor, parts: torch.Tensor, n_items: int, max_parts: int, xcds: int = 0):
+    def __init__(self, items: torch.Tensor, parts: torch.Tensor, n_items: int, max_parts: int, xcds: int = 0,
+                 kernel: int = 0):
         self.items, self.parts, self.n_items, self.max_parts = items, parts, n_items, max_parts
-        self.xcds = xcds
+        self.xcds, self.kernel = xcds, kernel
 
     def apply(self, p: _lib.AttendParams) -> None:
         p.work_items_dev, p.work_parts_dev = self.items.data_ptr(), self.parts.data_ptr()
         p.n_work_items, p.work_max_parts, p.work_xcds = self.n_items, self.max_parts, self.xcds
+        p.kernel = self.kernel
 
 
 def _kernel_group(group: int) -> int:
@@ -441,6 +447,16 @@ def _plan_xcds(p: _lib.AttendParams, device, single_launch: bool) -> int:
     return xcds if 1 < xcds <= 8 else 0
 
 
+def _plan_kernel(p: _lib.AttendParams, c_lens) -> int:
+    """The kernel value to plan and launch a list over these lengths with
+    (``hexkv_attend_plan_kernel``: the requested one, or for "auto" the
+    row-block kernel on large calls planned for the XCDs)."""
+    kernel = ctypes.c_int32()
+    _lib.check(_lib.load().hexkv_attend_plan_kernel(ctypes.byref(p), c_lens, ctypes.byref(kernel)),
+               "hexkv_attend_plan_kernel")
+    return kernel.value
+
+
 def _plan_work(p: _lib.AttendParams, lens: Sequence[int], device, single_launch: bool = True) -> WorkList:
     """Build the work list on the host (``hexkv_attend_plan``) and copy it to
     ``device`` on the current stream (asynchronously, from pinned memory).
@@ -455,17 +471,22 @@ def _plan_work(p: _lib.AttendParams, lens: Sequence[int], device, single_launch:
         raise ValueError(f"{len(lens)} host lengths for a batch of {p.batch}")
     p.work_xcds = _plan_xcds(p, device, single_launch)
     c_lens = (ctypes.c_int32 * len(lens))(*[int(n) for n in lens])
-    n_items, max_parts = ctypes.c_int32(), ctypes.c_int32()
-    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n_items),
-                                     ctypes.byref(max_parts)), "hexkv_attend_plan")
-    n_segs = p.batch * p.q_heads  # head groups never outnumber query heads
-    items = torch.empty((max(n_items.value, 1), 8), dtype=torch.int32, pin_memory=True)
-    parts = torch.empty(max(n_segs, 1), dtype=torch.int32, pin_memory=True)
-    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, ctypes.c_void_p(items.data_ptr()), items.shape[0],
-                                     ctypes.c_void_p(parts.data_ptr()), parts.shape[0], ctypes.byref(n_items),
-                                     ctypes.byref(max_parts)), "hexkv_attend_plan")
-    return WorkList(items.to(device, non_blocking=True), parts.to(device, non_blocking=True),
-                    n_items.value, max_parts.value, p.work_xcds)
+    requested = p.kernel
+    p.kernel = _plan_kernel(p, c_lens)
+    try:
+        n_items, max_parts = ctypes.c_int32(), ctypes.c_int32()
+        _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n_items),
+                                         ctypes.byref(max_parts)), "hexkv_attend_plan")
+        n_segs = p.batch * p.q_heads  # head groups never outnumber query heads
+        items = torch.empty((max(n_items.value, 1), 8), dtype=torch.int32, pin_memory=True)
+        parts = torch.empty(max(n_segs, 1), dtype=torch.int32, pin_memory=True)
+        _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, ctypes.c_void_p(items.data_ptr()),
+                                         items.shape[0], ctypes.c_void_p(parts.data_ptr()), parts.shape[0],
+                                         ctypes.byref(n_items), ctypes.byref(max_parts)), "hexkv_attend_plan")
+        return WorkList(items.to(device, non_blocking=True), parts.to(device, non_blocking=True),
+                        n_items.value, max_parts.value, p.work_xcds, p.kernel)
+    finally:
+        p.kernel = requested
 
 
 def decode_attention_noalloc(q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor, *, max_seqlen: int,
@@ -681,6 +702,7 @@ class AttendPlan:
         self.geometry = _plan_geometry(q, cache, out, kv_new)
         self.lens = None if lens is None else [int(n) for n in lens]
         self.work_key, self.work = None, None
+        self.kernel = self.params.kernel  # as requested; a work list sets the one its launches use
 
     def _grow_workspace(self) -> None:
         need = int(self.lib.hexkv_attend_workspace_bytes(ctypes.byref(self.params)))
@@ -694,7 +716,7 @@ class AttendPlan:
         p = self.params
         key = (int(seqlen_bias), int(max_seqlen))
         if key != self.work_key:
-            p.work_items_dev = None
+            p.work_items_dev, p.kernel = None, self.kernel
             self.work = _plan_work(p, self.lens, self.device, self.single_launch)
             self.work_key = key
         self.work.apply(p)
@@ -713,11 +735,11 @@ class AttendPlan:
     def reserve(self, lists: Sequence[WorkList]) -> None:
         """Grow the workspace once to fit every list in ``lists``."""
         p = self.params
-        saved = (p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds)
+        saved = (p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds, p.kernel)
         for work in lists:
             work.apply(p)
             self._grow_workspace()
-        (p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds) = saved
+        (p.work_items_dev, p.work_parts_dev, p.n_work_items, p.work_max_parts, p.work_xcds, p.kernel) = saved
 
     def check(self, q: torch.Tensor, cache: torch.Tensor, out: torch.Tensor,
               kv_new: Optional[torch.Tensor]) -> None:
@@ -758,7 +780,9 @@ class StepWorkLists:
     ``kv_new``), for t < ``steps``; each step is planned with its own chunk
     (``partition`` 0: the library's choice for that step, else the given
     one) and, with ``single_launch``, for the device's XCDs.  ``self[t]`` is
-    step t's ``WorkList``; ``chunks[t]`` its chunk.  Nothing is planned or
+    step t's ``WorkList``; ``chunks[t]`` its chunk and ``kernels[t]`` the
+    kernel value it was planned with (``hexkv_attend_plan_kernel``: the
+    row-block kernel for "auto" on large calls).  Nothing is planned or
     copied per step afterwards.
     """
 
@@ -779,9 +803,11 @@ class StepWorkLists:
         q.max_seqlen = max(self.lens, default=0) + steps - 1 + extra
         c_lens = (ctypes.c_int32 * len(self.lens))(*self.lens)
         n_segs = max(p.batch * p.q_heads, 1)  # head groups never outnumber query heads
-        sizes, self.chunks = [], []
+        requested = q.kernel
+        sizes, self.chunks, self.kernels = [], [], []
         for t in range(steps):
-            q.seqlen_bias = t
+            q.seqlen_bias, q.kernel, q.partition = t, requested, 0
+            q.kernel = _plan_kernel(q, c_lens)
             chunk, n, mp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
             q.partition = int(partition)
             _lib.check(lib.hexkv_attend_plan_chunk(ctypes.byref(q), c_lens, ctypes.byref(chunk)),
@@ -791,6 +817,7 @@ class StepWorkLists:
                                              ctypes.byref(mp)), "hexkv_attend_plan")
             sizes.append((max(n.value, 1), mp.value))
             self.chunks.append(chunk.value)
+            self.kernels.append(q.kernel)
         # one buffer: per step, its items (8 words each) then n_segs counts
         offsets, words = [], 0
         for n, _ in sizes:
@@ -799,15 +826,15 @@ class StepWorkLists:
         host = torch.zeros(words, dtype=torch.int32, pin_memory=True)
         base = host.data_ptr()
         for t, ((n, _), off) in enumerate(zip(sizes, offsets)):
-            q.seqlen_bias, q.partition = t, self.chunks[t]
+            q.seqlen_bias, q.partition, q.kernel = t, self.chunks[t], self.kernels[t]
             got, mp = ctypes.c_int32(), ctypes.c_int32()
             _lib.check(lib.hexkv_attend_plan(ctypes.byref(q), c_lens, ctypes.c_void_p(base + off * 4), n,
                                              ctypes.c_void_p(base + (off + n * 8) * 4), n_segs, ctypes.byref(got),
                                              ctypes.byref(mp)), "hexkv_attend_plan")
         self.device_buffer = host.to(device)
         self.lists = [WorkList(self.device_buffer[off:off + n * 8].view(n, 8),
-                               self.device_buffer[off + n * 8:off + n * 8 + n_segs], n, mp, q.work_xcds)
-                      for (n, mp), off in zip(sizes, offsets)]
+                               self.device_buffer[off + n * 8:off + n * 8 + n_segs], n, mp, q.work_xcds, k)
+                      for (n, mp), off, k in zip(sizes, offsets, self.kernels)]
         self.steps, self.xcds = steps, q.work_xcds
         self.max_parts = max(mp for _, mp in sizes)
         self.max_seqlen = q.max_seqlen

@@ -52,7 +52,12 @@ enum hexkv_dtype {
 enum hexkv_kernel {
   HEXKV_KERNEL_AUTO = 0,
   HEXKV_KERNEL_VALU = 1, /* packed dot products on the vector ALUs     */
-  HEXKV_KERNEL_MFMA = 2  /* scores and P.V on the matrix cores           */
+  HEXKV_KERNEL_MFMA = 2, /* scores and P.V on the matrix cores           */
+  HEXKV_KERNEL_ROWS = 3  /* work lists planned for the XCDs only: each item
+                            covers a block of adjacent KV heads (contiguous
+                            bytes of every cache row); 16-bit, head_dim 128,
+                            1, 2 or 4 query heads per KV head; see
+                            hexkv_attend_plan_kernel */
 };
 
 enum hexkv_status {
@@ -87,6 +92,8 @@ const char *hexkv_last_error(void);
                                           (work_xcds > 0), so its in-kernel merge may have read stale partials */
 #define HEXKV_STATUS_DISPATCH 8u       /* hexkv_attend, information only: a work item ran on another XCD than its
                                           index modulo work_xcds (the segment's items can still share one) */
+#define HEXKV_STATUS_LIST 16u          /* hexkv_attend: a work item planned for another head-group size (another
+                                          kernel) was skipped, so its outputs were not written */
 
 /*
  * Waits for `stream`, then reads the status word of the stream's device into
@@ -169,14 +176,16 @@ int hexkv_append(const void *kv_new, void *cache, int batch,
 /*
  * One workgroup's share of decode attention in a work list (32 bytes): the
  * `count` positions from `first` of query row `row` for the query heads of
- * head group `head_group` (head groups of hexkv_attend_plan's size), which
- * is partition `part` of the `parts` partitions that row and head group is
- * cut into.  `len` is the row's attended length (with kv_new, the new row
- * is position len - 1).
+ * head group `head_group` (head groups of `heads` query heads, the size
+ * hexkv_attend_plan planned for), which is partition `part` of the `parts`
+ * partitions that row and head group is cut into.  `len` is the row's
+ * attended length (with kv_new, the new row is position len - 1).  A launch
+ * whose head groups have another size skips the item and raises
+ * HEXKV_STATUS_LIST (`heads` 0: the launch's own size is assumed).
  */
 typedef struct hexkv_work_item {
   int32_t row, head_group, part, parts;
-  int32_t first, count, len, reserved;
+  int32_t first, count, len, heads;
 } hexkv_work_item;
 
 /*
@@ -279,7 +288,8 @@ int hexkv_attend(const hexkv_attend_params *p, void *workspace,
  * row b attends len_b = lens[b] + p->seqlen_bias (+1 with kv_new) keys,
  * each within [0, p->max_seqlen].  Every (row, head group) segment is cut
  * into chunks of p->partition positions (0: the library's choice by the
- * bytes the call reads, see hexkv_attend_plan_chunk; else a multiple of 64),
+ * bytes the call reads, see hexkv_attend_plan_chunk; else a multiple of 64,
+ * of 16 for HEXKV_KERNEL_ROWS, whose segments are blocks of KV heads),
  * and the items are ordered for the launch: empty
  * rows, then the full chunks across all segments, then each segment's last,
  * shorter chunk from the longest down.  With p->work_xcds = N > 0 the
@@ -323,6 +333,22 @@ int hexkv_attend_plan(const hexkv_attend_params *p, const int32_t *lens, hexkv_w
  * reference (it has no planning step).
  */
 int hexkv_attend_plan_chunk(const hexkv_attend_params *p, const int32_t *lens, int32_t *chunk);
+
+/*
+ * The kernel value to plan and launch these lengths with: p->kernel when it
+ * is not HEXKV_KERNEL_AUTO; for AUTO, HEXKV_KERNEL_ROWS when the call reads
+ * at least 64 MB, fits the row-block kernel and is planned for the XCDs
+ * (p->work_xcds 1-8), else AUTO's own choice (HEXKV_KERNEL_VALU or _MFMA).
+ * The row-block kernel streams 2 adjacent KV heads per item for grouped
+ * queries, 8 for one query head per KV head, and reads those heads' bytes of
+ * every cache row contiguously; at Llama-3-8B's and Llama-2-7B's shapes it
+ * measured 7-8% and ~4% faster per call than one head per item.  A caller
+ * sets the returned value in p->kernel for hexkv_attend_plan and for the
+ * launches of that list.  Returns HEXKV_OK with *kernel set, or an error as
+ * hexkv_attend_plan.  No counterpart in the reference (it has no planning
+ * step).
+ */
+int hexkv_attend_plan_kernel(const hexkv_attend_params *p, const int32_t *lens, int32_t *kernel);
 
 /* Size of the static scratch array behind hexkv_attend_noalloc (per GPU). */
 #define HEXKV_NOALLOC_SCRATCH_BYTES (32u << 20)

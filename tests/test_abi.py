@@ -153,7 +153,8 @@ def test_cpu_tensors_are_rejected_loudly():
     (8, 1, 128, torch.float32, "auto", "valu"),      # fp32 never takes the matrix cores
     (8, 1, 32, torch.float16, "auto", "valu"),       # head_dim below 64
     (8, 1, 128, torch.bfloat16, "valu", "valu"),
-    (32, 8, 128, torch.bfloat16, "mfma", "mfma")])
+    (32, 8, 128, torch.bfloat16, "mfma", "mfma"),
+    (32, 8, 128, torch.bfloat16, "rows", "rows")])
 def test_attend_kernel_choice(hq, hkv, d, dtype, kernel, expect):
     """hexkv_attend_kernel resolves the kernel choice from geometry alone
     (no device memory is touched)."""
@@ -237,3 +238,32 @@ def test_single_launch_and_lengths_out_validation():
     assert b"lengths_out_dev" in lib.hexkv_last_error()
     assert lib.hexkv_device_status(None, 0, None) == _lib.HEXKV_EINVAL
     assert lib.hexkv_device_xcds(None) == _lib.HEXKV_EINVAL
+
+
+def test_row_block_kernel_validation():
+    """HEXKV_KERNEL_ROWS is refused before any launch outside what it runs:
+    work lists planned for 1-8 XCDs with at most 64 partitions per segment,
+    16-bit data, head_dim 128, 2+ KV heads and 1, 2 or 4 query heads each."""
+    lib = _lib.load()
+
+    def params(**kw):
+        g = dict(dtype=1, batch=1, q_len=1, q_heads=32, kv_heads=8, head_dim=128, capacity=8, max_seqlen=4,
+                 softmax_scale=0.125, q=256, cache=256, out=256, cache_batch_stride=8 * 2 * 8 * 128,
+                 cache_pos_stride=2 * 8 * 128, cache_kv_stride=8 * 128, kernel=3, work_items_dev=256,
+                 work_parts_dev=256, n_work_items=1, work_max_parts=2, work_xcds=8)
+        g.update(kw)
+        return _lib.AttendParams(**g)
+
+    for kw in (dict(work_items_dev=None, work_parts_dev=None, work_xcds=0),  # grid mode
+               dict(work_xcds=0),                                           # not planned for the XCDs
+               dict(work_max_parts=65),                                     # more pieces than the merge takes
+               dict(dtype=2, cache_batch_stride=8 * 2 * 8 * 128),           # fp32
+               dict(head_dim=64, cache_batch_stride=8 * 2 * 8 * 64, cache_pos_stride=2 * 8 * 64,
+                    cache_kv_stride=8 * 64),                                # head_dim 64
+               dict(q_heads=8, kv_heads=1, cache_batch_stride=8 * 2 * 128, cache_pos_stride=2 * 128,
+                    cache_kv_stride=128),                                   # one KV head
+               dict(q_heads=64)):                                           # group 8
+        assert lib.hexkv_attend(ctypes.byref(params(**kw)), None, 0, None) == _lib.HEXKV_EUNSUPPORTED, kw
+    p = params(kernel=4)
+    assert lib.hexkv_attend(ctypes.byref(p), None, 0, None) == _lib.HEXKV_EINVAL
+    assert lib.hexkv_attend_kernel(ctypes.byref(params())) == _lib.KERNELS["rows"]

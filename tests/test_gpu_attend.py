@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from hexgen2_amd import ops
+from hexgen2_amd import _lib, ops
 from oracle import kv_oracle as oracle
 
 pytestmark = pytest.mark.gpu
@@ -302,6 +302,93 @@ def test_output_at_odd_element_offset(device, hq, hkv, d, dtype, kernel):
         assert buf[0].item() == 5.0
         assert (aligned[0] == 0).all()
         check(aligned[1:], q[1:], cache[1:], lens[1:], dtype)
+
+
+# (hq, hkv, dtype): geometries of the row-block kernel (head_dim 128): items
+# of 2 adjacent KV heads for grouped queries, 8 (or 4) for one query head
+# per KV head
+ROWS_GEOMETRIES = [
+    (32, 8, torch.bfloat16),   # Llama-3-8B
+    (32, 8, torch.float16),
+    (32, 32, torch.float16),   # Llama-2-7B: 8 KV heads per item
+    (16, 8, torch.bfloat16),   # group 2
+    (8, 4, torch.bfloat16),    # group 2, 2 blocks per row
+    (4, 4, torch.float16),     # group 1, 4 KV heads: one block of 4
+]
+
+
+@pytest.mark.parametrize("hq,hkv,dtype", ROWS_GEOMETRIES)
+def test_row_block_kernel_ragged_within_tolerance(device, hq, hkv, dtype):
+    """The row-block kernel over ragged lists (empty rows, single keys,
+    rows ending on and around chunk boundaries, up to 64 pieces per row
+    merged in the kernel): within tolerance of the oracle, the fused append
+    bit-exact, and the device status clear."""
+    lens = [0, 1, 15, 16, 17, 63, 64, 65, 700, 1500, 2047, 2048]
+    cap = 2112
+    print(f"row-block hq={hq} hkv={hkv} {dtype}", flush=True)
+    q, cache = make(len(lens), cap, hq, hkv, 128, dtype, 43, device)
+    g = torch.Generator(device=device).manual_seed(44)
+    kv_new = torch.randn((len(lens), 2, hkv, 128), generator=g, device=device).to(dtype)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    want_cache = oracle.append(bits(cache), bits(kv_new), lens)
+    ops.device_status()
+    for partition in (0, 48, 144, 512):
+        c = cache.clone()
+        out = ops.decode_attention(q, c, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new,
+                                   partition=partition, kernel="rows", lens=lens)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits(c), want_cache)
+        check(out, q, c, [n + 1 for n in lens], dtype)
+    out = torch.full_like(q, 9.0)
+    ops.decode_attention(q, cache, max_seqlen=max(lens), seqlens=seqlens, kernel="rows", lens=lens, out=out)
+    assert (out[0] == 0).all()
+    check(out[1:], q[1:], cache[1:], lens[1:], dtype)
+    assert ops.device_status() & _lib.STATUS_ERRORS == 0
+
+
+@pytest.mark.parametrize("hq,hkv,dtype", ROWS_GEOMETRIES[:3])
+def test_row_block_kernel_agrees_with_head_items(device, hq, hkv, dtype):
+    """Row-block and one-head-per-item lists of the same call: outputs within
+    the bf16/fp16 tolerance of each other, caches bit-identical."""
+    lens = [300, 5, 1200, 77, 2500, 640, 0, 4095]
+    q, cache = make(len(lens), 4160, hq, hkv, 128, dtype, 45, device)
+    g = torch.Generator(device=device).manual_seed(46)
+    kv_new = torch.randn((len(lens), 2, hkv, 128), generator=g, device=device).to(dtype)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    c_rows, c_head = cache.clone(), cache.clone()
+    o_rows = ops.decode_attention(q, c_rows, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new,
+                                  kernel="rows", lens=lens)
+    o_head = ops.decode_attention(q, c_head, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new,
+                                  kernel="valu", lens=lens)
+    torch.cuda.synchronize()
+    assert torch.equal(c_rows.view(torch.int16), c_head.view(torch.int16))
+    torch.testing.assert_close(o_rows.float(), o_head.float(), rtol=0, atol=TOL[dtype])
+
+
+def test_list_planned_for_another_kernel_is_skipped_and_reported(device):
+    """A row-block list launched as the one-head-per-item kernel (head groups
+    of another size): every item is skipped, nothing is written, and the
+    status word says so (check_device_status raises)."""
+    lens = [100, 900, 33]
+    q, cache = make(len(lens), 1024, 32, 8, 128, torch.bfloat16, 47, device)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    out = torch.full_like(q, 7.0)
+    plan = ops.AttendPlan(q, cache, out, max_seqlens=[max(lens)], seqlens=seqlens, kernel="rows")
+    work = ops._plan_work(plan.params, lens, device)
+    assert work.kernel == _lib.KERNELS["rows"]
+    plan.fix_work_list(work)
+    plan.params.kernel = _lib.KERNELS["valu"]  # launch it as another kernel
+    ops.device_status()
+    plan(q, cache, out, None, 0, max(lens))
+    torch.cuda.synchronize()
+    assert (out == 7.0).all(), "a skipped item wrote"
+    with pytest.raises(ValueError, match="another attention kernel"):
+        ops.check_device_status()
+    assert ops.device_status() == 0  # the check cleared it
+    plan.params.kernel = work.kernel  # as planned: every output written
+    plan(q, cache, out, None, 0, max(lens))
+    check(out, q, cache, lens, torch.bfloat16)
+    assert ops.device_status() & _lib.STATUS_ERRORS == 0
 
 
 @pytest.mark.parametrize("kernel", ["valu", "mfma"])

@@ -67,6 +67,9 @@ def test_graph_replays_match_eager_steps(device, hq, hkv, d, dtype, kernel):
             assert changed.sum() <= len(lens)
 
 
+KERNEL_NAMES = {v: k for k, v in _lib.KERNELS.items()}
+
+
 @pytest.mark.parametrize("hq,hkv,d,dtype,kernel,partition,single", [
     (32, 8, 128, torch.bfloat16, "valu", 64, True),
     (32, 8, 128, torch.bfloat16, "mfma", 128, True),
@@ -74,7 +77,9 @@ def test_graph_replays_match_eager_steps(device, hq, hkv, d, dtype, kernel):
     (8, 1, 128, torch.bfloat16, "auto", 0, True),
     (32, 4, 64, torch.float16, "auto", 0, True),
     (32, 4, 64, torch.float16, "auto", 64, False),
-    (4, 4, 16, torch.float32, "auto", 64, True)])
+    (4, 4, 16, torch.float32, "auto", 64, True),
+    (32, 8, 128, torch.bfloat16, "rows", 32, True),
+    (32, 32, 128, torch.float16, "rows", 0, True)])
 def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, kernel, partition, single):
     """DecodeStepGraph(lens=...): every step's work list is planned up front
     (StepWorkLists) and captured in a graph of its own, and the last layer's
@@ -99,10 +104,11 @@ def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, ke
     pos_e = torch.tensor(lens, dtype=torch.int32, device=device)
     host = list(lens)
 
-    def eager_step(chunk):
+    def eager_step(chunk, step_kernel):
         for l in range(layers):
             ops.decode_attention(q[l], cache_e[l], max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[l],
-                                 out=out_e[l], kernel=kernel, lens=host, partition=chunk, single_launch=single)
+                                 out=out_e[l], kernel=step_kernel, lens=host, partition=chunk,
+                                 single_launch=single)
         pos_e.add_(1)
         host[:] = [n + 1 for n in host]
 
@@ -112,7 +118,7 @@ def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, ke
 
     ops.device_status()  # start clear
     refill()
-    eager_step(partition)  # also loads the kernels before capture
+    eager_step(partition, kernel)  # also loads the kernels before capture
     cache_g.copy_(cache_e)
     pos_g = pos_e.clone()
     torch.cuda.synchronize()
@@ -122,10 +128,12 @@ def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, ke
     assert len(lists) == steps - 1 and (lists.xcds > 0) == single
     if partition:
         assert set(lists.chunks) == {partition}
+    if kernel != "auto":
+        assert set(lists.kernels) == {_lib.KERNELS[kernel]}
     counts = []
     for step in range(steps - 1):
         refill()
-        eager_step(lists.chunks[step])
+        eager_step(lists.chunks[step], KERNEL_NAMES[lists.kernels[step]])  # as the step was planned
         graph.replay()
         torch.cuda.synchronize()
         counts.append(int(lists[step].parts.sum()))  # partitions over all segments

@@ -168,6 +168,9 @@ def test_llama3_8b_full_handoff_round_trip(device):
     torch.cuda.empty_cache()
 
 
+KERNEL_NAMES = {v: k for k, v in _lib.KERNELS.items()}
+
+
 @pytest.mark.timeout(600)
 @pytest.mark.parametrize("name", ["tinyllama-1.1b", "llama2-7b", "llama2-70b-tp8", "llama3-8b"])
 def test_graph_work_lists_at_full_size(device, name):
@@ -203,15 +206,16 @@ def test_graph_work_lists_at_full_size(device, name):
     torch.cuda.synchronize()
     graph = ops.DecodeStepGraph(q, cache_g, out_g, kv_new, pos_g, max_seqlen, lens=host)
     lists = graph.lists
-    print(f"  chunks {lists.chunks}, items {[lst.n_items for lst in lists.lists]}, partitions {lists.max_parts}, "
-          f"XCDs {lists.xcds}", flush=True)
+    kernels = [KERNEL_NAMES[k] for k in lists.kernels]
+    print(f"  chunks {lists.chunks}, kernels {kernels}, items {[lst.n_items for lst in lists.lists]}, "
+          f"partitions {lists.max_parts}, XCDs {lists.xcds}", flush=True)
     assert len(lists) == replays and len(graph.graphs) == replays
     for step in range(replays):
         q.normal_(generator=g)
         kv_new.normal_(generator=g)
         for l in range(layers):
             ops.decode_attention(q[l], cache_e[l], max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[l],
-                                 out=out_e[l], lens=host, partition=lists.chunks[step])
+                                 out=out_e[l], lens=host, partition=lists.chunks[step], kernel=kernels[step])
         pos_e.add_(1)
         host = [n + 1 for n in host]
         graph.replay()

@@ -88,7 +88,7 @@ def plan(p, lens):
     _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, items, n.value, parts, len(parts),
                                      ctypes.byref(n2), ctypes.byref(mp2)), "plan")
     assert (n2.value, mp2.value) == (n.value, mp.value)
-    arr = np.array([[it.row, it.head_group, it.part, it.parts, it.first, it.count, it.len, it.reserved]
+    arr = np.array([[it.row, it.head_group, it.part, it.parts, it.first, it.count, it.len, it.heads]
                     for it in items[:n.value]], dtype=np.int64)
     return arr, np.array(parts[:]), mp.value
 
@@ -393,3 +393,123 @@ def test_small_calls_split_when_merged_in_kernel():
     assert len(arr) == 80  # 4 XCDs with one segment's 10 items, 4 with padding only
     rc, chunk = plan_chunk(p, [4000])
     assert rc == 0 and chunk == 384
+
+
+# ------------------------------------------------------- row-block lists ---
+
+def rows_params(batch, hq, hkv, dtype=_lib.HEXKV_BF16, partition=0, xcds=8):
+    p = params(batch, hq, hkv, 128, dtype=dtype, partition=partition)
+    p.kernel, p.work_xcds = _lib.KERNELS["rows"], xcds
+    return p
+
+
+def rows_block(hq, hkv):
+    group = hq // hkv
+    if group > 1:
+        return 2
+    return next(hb for hb in (8, 4, 2) if hkv % hb == 0)
+
+
+@pytest.mark.parametrize("lens,hq,hkv", [
+    ([7897, 221, 4000, 1023, 1024, 1025, 0, 5000], 32, 8),  # Llama-3-8B geometry: 2 KV heads per item
+    ([2000, 300, 1500, 256, 64, 0, 1999, 777], 32, 32),     # Llama-2-7B geometry: 8 KV heads per item
+    ([900, 17, 3], 8, 4),                                   # group 2
+    ([513, 1, 60], 4, 4),                                   # group 1, 4 KV heads: 4 per item
+])
+def test_row_block_plans_cover_every_position_once(lens, hq, hkv):
+    """Row-block lists: segments of hb adjacent KV heads (hb * group query
+    heads, recorded in every item), every attended position of every segment
+    once, each segment on one XCD, at most 64 pieces per segment."""
+    pieces = -(-(max(lens) + 1) // 64)  # 64 pieces of the longest row at most
+    finest = max(16, (pieces + 15) // 16 * 16)
+    for partition in (0, finest, 3 * finest):
+        p = rows_params(len(lens), hq, hkv, partition=partition)
+        arr, parts, max_parts = plan(p, lens)
+        heads = rows_block(hq, hkv) * (hq // hkv)
+        real = arr[arr[:, 0] < len(lens)]
+        assert (real[:, 7] == heads).all(), "items record their head-group size"
+        groups = hq // heads
+        att = [n + 1 for n in lens]
+        seen = {}
+        for i, (row, hg, part, nparts, first, count, length, _) in enumerate(arr):
+            if row >= len(lens):
+                continue  # padding
+            assert 0 <= hg < groups and length == att[row] and nparts == parts[row * groups + hg]
+            seen.setdefault((row, hg), []).append((first, count, i % 8))
+        for row in range(len(lens)):
+            for hg in range(groups):
+                spans = sorted(seen[(row, hg)])
+                assert len({x for _, _, x in spans}) == 1, "a segment's items share one XCD"
+                pos = 0
+                for first, count, _ in spans:
+                    assert first == pos
+                    pos += count
+                assert pos == att[row]
+        assert max_parts <= 64
+
+
+def test_row_block_chunk_rule():
+    """Chunks of about 1/400 of the call's head-block positions at the
+    measured shapes (400-550 items with each segment's shorter last piece),
+    in multiples of 16 positions, and never more than 64 pieces per row."""
+    from hexgen2_amd.workloads import workload
+    for name, hq, hkv in (("llama3-8b", 32, 8), ("llama2-7b", 32, 32)):
+        w = workload(name)
+        p = rows_params(w.batch, hq, hkv, dtype=_lib.HEXKV_BF16 if name == "llama3-8b" else _lib.HEXKV_F16)
+        arr, _, max_parts = plan(p, w.lens)
+        real = arr[arr[:, 0] < w.batch]
+        rc, chunk = plan_chunk(p, w.lens)
+        assert rc == 0 and chunk % 16 == 0
+        assert 330 <= len(real) <= 560, (name, len(real))
+        assert max_parts <= 64
+    # one long row: the chunk grows so that the row has at most 64 pieces
+    p = rows_params(1, 32, 8)
+    for n in (100000, 1036, 1500, 4095):
+        rc, chunk = plan_chunk(p, [n])
+        assert rc == 0 and chunk % 16 == 0 and (n + 1 + chunk - 1) // chunk <= 64, (n, chunk)
+    # a forced partition that would need more pieces is refused
+    p = rows_params(1, 32, 8, partition=16)
+    rc, _ = plan_chunk(p, [5000])
+    assert rc == _lib.HEXKV_EUNSUPPORTED
+
+
+def plan_kernel(p, lens):
+    lib = _lib.load()
+    c_lens = (ctypes.c_int32 * len(lens))(*lens)
+    k = ctypes.c_int32()
+    rc = lib.hexkv_attend_plan_kernel(ctypes.byref(p), c_lens, ctypes.byref(k))
+    return rc, k.value
+
+
+def test_plan_kernel_choice():
+    """hexkv_attend_plan_kernel: the row-block kernel for "auto" on calls of
+    64 MB or more that fit it and are planned for the XCDs; AUTO's own
+    choice otherwise; an explicit kernel as given."""
+    from hexgen2_amd.workloads import workload
+    K = _lib.KERNELS
+    w = workload("llama3-8b")
+    p = params(w.batch, 32, 8, 128)
+    p.work_xcds = 8
+    assert plan_kernel(p, w.lens) == (0, K["rows"])
+    p.work_xcds = 0  # merged by a second launch: not the row-block kernel
+    assert plan_kernel(p, w.lens) == (0, K["valu"])
+    p.work_xcds, p.kernel = 8, K["valu"]
+    assert plan_kernel(p, w.lens) == (0, K["valu"])
+    w = workload("llama2-7b")
+    p = params(w.batch, 32, 32, 128, dtype=_lib.HEXKV_F16)
+    p.work_xcds = 8
+    assert plan_kernel(p, w.lens) == (0, K["rows"])
+    # small calls, one KV head, fp32, head_dim 64: AUTO's own choice
+    p = params(2, 32, 8, 128)
+    p.work_xcds = 8
+    assert plan_kernel(p, [100, 200]) == (0, K["valu"])
+    w = workload("llama2-70b-tp8")
+    p = params(w.batch, 8, 1, 128)
+    p.work_xcds = 8
+    assert plan_kernel(p, w.lens) == (0, K["mfma"])
+    p = params(64, 32, 8, 128, dtype=_lib.HEXKV_F32)
+    p.work_xcds = 8
+    assert plan_kernel(p, [8000] * 64) == (0, K["valu"])
+    p = params(64, 32, 8, 64)
+    p.work_xcds = 8
+    assert plan_kernel(p, [8000] * 64)[1] != K["rows"]

@@ -1699,6 +1699,26 @@ static int dispatch_d(int D, int G, const AttendArgs &a, dim3 grid, int kind, hi
 
 namespace hexkv {
 
+// Home XCD of each (row, head group) segment of a list planned for X XCDs
+// (segment s = row * groups + group, len[row] positions): longest first,
+// each to the XCD with the fewest positions so far.  All 0 for X = 1.
+static std::vector<int> segment_homes(const std::vector<int64_t> &len, int groups, int X) {
+  const int64_t segs = static_cast<int64_t>(len.size()) * groups;
+  std::vector<int> home(static_cast<size_t>(segs), 0);
+  if (X <= 1) return home;
+  std::vector<int64_t> order(static_cast<size_t>(segs));
+  for (int64_t i = 0; i < segs; ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t x, int64_t y) { return len[x / groups] > len[y / groups]; });
+  std::vector<int64_t> load(X, 0);
+  for (const int64_t sg : order) {
+    const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    home[sg] = x;
+    load[x] += std::max<int64_t>(len[sg / groups], 1);
+  }
+  return home;
+}
+
 // Chunk size (positions) of a work list when the caller leaves the choice to
 // the library, by the bytes one call reads (W positions over all (row, head
 // group) segments, row_bytes per position of one KV head).  Measured on
@@ -1732,6 +1752,62 @@ static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest, boo
   if (bytes < (INT64_C(4) << 20)) return static_cast<int>(std::max<int64_t>(64, (longest + 63) / 64 * 64));
   if (bytes < (INT64_C(64) << 20)) return static_cast<int>(std::min<int64_t>(1024, std::max<int64_t>(64, (positions / 240 + 63) / 64 * 64)));
   return positions >= (INT64_C(1) << 20) ? 1280 : 896;
+}
+
+// Chunk of a row-block list (positions, a multiple of 16).  Each XCD runs
+// its share of the list in order on its 32 CUs, as many workgroups per CU
+// at once as registers and LDS allow (4 for 4 query heads per KV head: 103
+// VGPRs and 33 KB of LDS; 5 otherwise: 84 VGPRs), so the first
+// kRowsSlots items of a share start together and each later one starts
+// when a slot frees.  A share is its segments' full chunks (all the same
+// size), then their shorter last pieces from the longest down.  The chunk
+// is the smallest one at which no share holds more than 27/32 of its slots
+// in full chunks: the full chunks all start at once, and the slots left
+// over hold the longest last pieces, which finish early and hand their
+// slots to the short ones still waiting.  Measured on MI355X at Llama-3-8B
+// (one layer, decode steps 0-255, HBM-resident, interleaved A/B in one
+// process): 107-109 full chunks in a share of 128 slots 149.8-159.8 us per
+// call (0.83 of 8 TB/s), 109-111 153.3-164.3, 113 or more 166.6-178.1 (the
+// last pieces then wait for the full chunks: a second round), 95-102
+// 157.8-168.1 (fewer, longer full chunks per CU); the earlier target of
+// ~400 items (528 with the last pieces) 154.9-162.5; this rule 152.4-160.6.
+// A model of the dispatch (each share in order onto 128 slots, each CU's
+// bandwidth shared by its items) puts the best chunk at the same place and
+// the cliff on its finer side, hence the margin.  Small calls are bound by
+// each item's fixed latency instead: no item under kRowsItemBytes
+// (Llama-2-7B, 8-head items of 4 KB per position: 112 positions, ~400
+// items, 29.7-31.3 us per call over decode steps 0-63, against 33.2-35.2 at
+// 80-96 and 34.8-37.2 at 64).  At most kMergeMaxParts pieces per row.
+constexpr int kCusPerXcd = 32;
+constexpr int64_t kRowsItemBytes = INT64_C(448) << 10;
+
+static int rows_chunk(const hexkv_attend_params *p, const int32_t *lens, int hb, int64_t longest) {
+  const int groups = p->kv_heads / hb;
+  const int X = std::max(1, p->work_xcds);
+  const int extra = p->kv_new ? 1 : 0;
+  std::vector<int64_t> len(p->batch);
+  for (int b = 0; b < p->batch; ++b) len[b] = static_cast<int64_t>(lens[b]) + p->seqlen_bias + extra;
+  const std::vector<int> home = segment_homes(len, groups, X);
+  const int64_t per_cu = p->q_heads / p->kv_heads == 4 ? 4 : 5;
+  const int64_t full_limit = kCusPerXcd * per_cu * 27 / 32;
+  const int64_t block_bytes = 2 * static_cast<int64_t>(hb) * p->head_dim * elem_size(p->dtype);
+  const int64_t fewest = (longest + kMergeMaxParts - 1) / kMergeMaxParts;  // positions per piece
+  auto up16 = [](int64_t v) { return (v + 15) / 16 * 16; };
+  const int64_t lo = std::max<int64_t>({16, up16((kRowsItemBytes + block_bytes - 1) / block_bytes), up16(fewest)});
+  auto fits = [&](int64_t c) {
+    std::vector<int64_t> full(X, 0);
+    for (size_t sg = 0; sg < home.size(); ++sg) full[home[sg]] += len[sg / groups] / c;
+    return *std::max_element(full.begin(), full.end()) <= full_limit;
+  };
+  // full chunks per share only fall as the chunk grows: binary search over
+  // multiples of 16 in [lo, hi], hi past the longest row (no full chunk)
+  int64_t a = lo / 16, z = std::max(lo, up16(longest + 1)) / 16;
+  if (fits(a * 16)) return static_cast<int>(a * 16);
+  while (z - a > 1) {
+    const int64_t m = (a + z) / 2;
+    (fits(m * 16) ? z : a) = m;
+  }
+  return static_cast<int>(z * 16);
 }
 
 // Checks a planning request and returns the chunk hexkv_attend_plan cuts
@@ -1774,16 +1850,7 @@ static int plan_request(const hexkv_attend_params *p, const int32_t *lens, const
   }
   const int64_t row_bytes = 2 * static_cast<int64_t>(p->head_dim) * elem_size(p->dtype);
   if (hb == 1) return plan_chunk(positions, row_bytes, longest, p->work_xcds > 0);
-  // Row-block lists: about kRowsItems items (measured best at both shapes
-  // the kernel was tuned on: Llama-3-8B 152-164 us per call at ~400 items
-  // of 2 heads, 178-181 at ~200 and 153-164 at ~800; Llama-2-7B 29.9-31.3 at
-  // ~400 items of 8 heads, 41 at ~200), in multiples of 16 positions, with
-  // at most kMergeMaxParts pieces per row.
-  constexpr int64_t kRowsItems = 400;
-  const int64_t block_positions = positions / hb;  // positions x head blocks
-  const int64_t fewest = (longest + kMergeMaxParts - 1) / kMergeMaxParts;  // positions per piece
-  const int64_t c = std::max<int64_t>({16, (block_positions / kRowsItems + 15) / 16 * 16, (fewest + 15) / 16 * 16});
-  return static_cast<int>(c);
+  return rows_chunk(p, lens, hb, longest);
 }
 
 }  // namespace hexkv
@@ -1852,21 +1919,7 @@ static int build_plan(const hexkv_attend_params *p, const int32_t *lens, int64_t
     for (int hg = 0; hg < groups; ++hg)
       seg_parts[static_cast<size_t>(b) * groups + hg] = static_cast<int32_t>(len[b] == 0 ? 1 : (len[b] + chunk - 1) / chunk);
 
-  // Home XCD of each segment (all on XCD 0 without XCD placement): longest
-  // first, each to the XCD with the fewest positions so far.
-  std::vector<int> home(static_cast<size_t>(segs), 0);
-  if (X > 1) {
-    std::vector<int64_t> order(static_cast<size_t>(segs));
-    for (int64_t i = 0; i < segs; ++i) order[i] = i;
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int64_t x, int64_t y) { return len[x / groups] > len[y / groups]; });
-    std::vector<int64_t> load(X, 0);
-    for (const int64_t sg : order) {
-      const int x = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
-      home[sg] = x;
-      load[x] += std::max<int64_t>(len[sg / groups], 1);
-    }
-  }
+  const std::vector<int> home = segment_homes(len, groups, X);
   // Each XCD's items: empty rows (a zero output each), then the full chunks,
   // chunk index by chunk index across its segments, then every segment's
   // last, shorter chunk from the longest down, so its share ends on its

@@ -448,20 +448,40 @@ def test_row_block_plans_cover_every_position_once(lens, hq, hkv):
         assert max_parts <= 64
 
 
+def full_chunks_per_xcd(arr, batch, chunk, xcds=8):
+    """Full chunks (count == chunk) in each XCD's share (item i runs on XCD i % xcds)."""
+    full = [0] * xcds
+    for i, it in enumerate(arr):
+        if it[0] < batch and it[5] == chunk:
+            full[i % xcds] += 1
+    return full
+
+
 def test_row_block_chunk_rule():
-    """Chunks of about 1/400 of the call's head-block positions at the
-    measured shapes (400-550 items with each segment's shorter last piece),
-    in multiples of 16 positions, and never more than 64 pieces per row."""
+    """The smallest chunk (a multiple of 16) at which no XCD's share holds
+    more than 27/32 of its 32 CUs' workgroup slots (4 per CU with 4 query
+    heads per KV head, 5 otherwise) in full chunks, with items of at least
+    448 KiB and at most 64 pieces per row: at Llama-3-8B's decode steps
+    ~1,100 items (1 KB per position), at Llama-2-7B's 112-position items (4
+    KB per position)."""
     from hexgen2_amd.workloads import workload
-    for name, hq, hkv in (("llama3-8b", 32, 8), ("llama2-7b", 32, 32)):
+    for name, hq, hkv, dtype, limit, floor, window in (
+            ("llama3-8b", 32, 8, _lib.HEXKV_BF16, 108, 448, (1000, 1200)),
+            ("llama2-7b", 32, 32, _lib.HEXKV_F16, 135, 112, (330, 480))):
         w = workload(name)
-        p = rows_params(w.batch, hq, hkv, dtype=_lib.HEXKV_BF16 if name == "llama3-8b" else _lib.HEXKV_F16)
-        arr, _, max_parts = plan(p, w.lens)
-        real = arr[arr[:, 0] < w.batch]
-        rc, chunk = plan_chunk(p, w.lens)
-        assert rc == 0 and chunk % 16 == 0
-        assert 330 <= len(real) <= 560, (name, len(real))
-        assert max_parts <= 64
+        for t in (0, w.decode_steps // 2, w.decode_steps - 1):
+            lens = [n + t for n in w.lens]
+            p = rows_params(w.batch, hq, hkv, dtype=dtype)
+            rc, chunk = plan_chunk(p, lens)
+            assert rc == 0 and chunk % 16 == 0 and chunk >= floor
+            arr, _, max_parts = plan(p, lens)
+            assert window[0] <= int((arr[:, 0] < w.batch).sum()) <= window[1], (name, t, len(arr))
+            assert max_parts <= 64
+            assert max(full_chunks_per_xcd(arr, w.batch, chunk)) <= limit
+            if chunk > floor:  # one step finer would overfill a share
+                finer = rows_params(w.batch, hq, hkv, dtype=dtype, partition=chunk - 16)
+                arr2, _, _ = plan(finer, lens)
+                assert max(full_chunks_per_xcd(arr2, w.batch, chunk - 16)) > limit, (name, t, chunk)
     # one long row: the chunk grows so that the row has at most 64 pieces
     p = rows_params(1, 32, 8)
     for n in (100000, 1036, 1500, 4095):

@@ -36,6 +36,8 @@ int symbol_address(const void *symbol, std::atomic<void *> *cache, hexkv_stream_
 // Device address of the status word (HEXKV_STATUS_* bits) of the device that
 // runs `stream`.
 int status_word(hexkv_stream_t stream, unsigned int **word, const char *what);
+// The XCD count of the stream's device (cached per device).
+int stream_xcds(hexkv_stream_t stream, int *xcds, const char *what);
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

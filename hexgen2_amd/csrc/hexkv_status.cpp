@@ -35,6 +35,22 @@ int stream_device(hexkv_stream_t stream, int *dev, const char *what) {
   return HEXKV_OK;
 }
 
+int stream_xcds(hexkv_stream_t stream, int *xcds, const char *what) {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  int rc = stream_device(stream, &dev, what);
+  if (rc != HEXKV_OK) return rc;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev);
+    if (e != hipSuccess) return fail(HEXKV_EHIP, "%s: XCD count of device %d: %s", what, dev, hipGetErrorString(e));
+    n = n > 0 ? n : 1;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  *xcds = n;
+  return HEXKV_OK;
+}
+
 static std::mutex g_symbol_mu;
 
 int symbol_address(const void *symbol, std::atomic<void *> *cache, hexkv_stream_t stream, void **addr,

@@ -90,8 +90,9 @@ const char *hexkv_last_error(void);
                                           (with kv_new, a new row past that bound was neither written nor attended) */
 #define HEXKV_STATUS_PLACEMENT 4u      /* hexkv_attend: the items of a split segment ran on more than one XCD
                                           (work_xcds > 0), so its in-kernel merge may have read stale partials */
-#define HEXKV_STATUS_DISPATCH 8u       /* hexkv_attend, information only: a work item ran on another XCD than its
-                                          index modulo work_xcds (the segment's items can still share one) */
+#define HEXKV_STATUS_DISPATCH 8u       /* hexkv_attend, information only: workgroup i started on another XCD
+                                          than i modulo work_xcds (the queue's dispatch starts elsewhere; the
+                                          items still run on the XCDs they were planned for) */
 #define HEXKV_STATUS_LIST 16u          /* hexkv_attend: a work item planned for another head-group size (another
                                           kernel) was skipped, so its outputs were not written */
 
@@ -241,10 +242,14 @@ typedef struct hexkv_attend_params {
    * 0: the partials of a split (row, head group) are merged by a second
    * kernel on the same stream.  N > 0 (the device's XCD count,
    * hexkv_device_xcds): every item of a split segment sits at one index
-   * modulo N, so -- workgroups reach the N XCDs round-robin by index -- its
-   * items share one XCD's L2, and the segment's last item to finish merges
-   * the partials inside the attention kernel: one launch per call.  Each
-   * workgroup checks its XCD and raises HEXKV_STATUS_PLACEMENT otherwise. */
+   * modulo N, so its items share one XCD's L2, and the segment's last item
+   * to finish merges the partials inside the attention kernel: one launch
+   * per call.  Workgroups reach the XCDs round-robin by index from a start
+   * XCD that depends on the hardware queue; when N divides the device's XCD
+   * count and the list length is a multiple of N (as planned), each
+   * workgroup runs the item of its own XCD within its group of N, so index
+   * j * N + x always runs on XCD x.  Each workgroup checks its XCD and raises
+   * HEXKV_STATUS_PLACEMENT if a segment's items still met on two. */
   int32_t work_xcds;
   /* Work-list calls with kv_new only, else NULL: row b's new cached length
    * (its attended keys, the appended row included) is stored to

@@ -365,6 +365,37 @@ def test_row_block_kernel_agrees_with_head_items(device, hq, hkv, dtype):
     torch.testing.assert_close(o_rows.float(), o_head.float(), rtol=0, atol=TOL[dtype])
 
 
+@pytest.mark.parametrize("kernel", ["valu", "mfma", "rows"])
+def test_work_list_same_on_every_stream(device, kernel):
+    """Workgroups reach the XCDs round-robin from a start XCD that depends on
+    the hardware queue; the kernels run each XCD's share of a list on that
+    XCD whatever the start.  The same fused call on four streams (the queues
+    of one process start at different XCDs): outputs and caches bit-identical,
+    within tolerance of the oracle, no error flag (the placement flag among
+    them)."""
+    lens = [3000, 17, 1200, 640, 2047, 95, 4000, 333]
+    q, cache = make(len(lens), 4160, 32, 8, 128, torch.bfloat16, 48, device)
+    g = torch.Generator(device=device).manual_seed(49)
+    kv_new = torch.randn((len(lens), 2, 8, 128), generator=g, device=device).to(torch.bfloat16)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    streams = [torch.cuda.current_stream()] + [torch.cuda.Stream() for _ in range(3)]
+    ops.device_status()
+    results = []
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            c = cache.clone()
+            out = ops.decode_attention(q, c, max_seqlen=max(lens) + 1, seqlens=seqlens, kv_new=kv_new,
+                                       kernel=kernel, lens=lens)
+        torch.cuda.synchronize()
+        results.append((out, c))
+    for out, c in results[1:]:
+        assert torch.equal(out, results[0][0])
+        assert torch.equal(c.view(torch.int16), results[0][1].view(torch.int16))
+    check(results[0][0], q, results[0][1], [n + 1 for n in lens], torch.bfloat16)
+    assert ops.device_status() & _lib.STATUS_ERRORS == 0
+
+
 def test_list_planned_for_another_kernel_is_skipped_and_reported(device):
     """A row-block list launched as the one-head-per-item kernel (head groups
     of another size): every item is skipped, nothing is written, and the

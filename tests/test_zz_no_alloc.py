@@ -73,6 +73,16 @@ def both(q, cache, lens, kv_new, kernel, listed=None):
                                                    (torch.bfloat16, 8, 1, 128, "mfma"),
                                                    (torch.float16, 32, 4, 64, "mfma")])
 def test_noalloc_matches_workspace_entry_point(device, dtype, hq, hkv, d, kernel, listed):
+    compare_entry_points(device, dtype, hq, hkv, d, kernel, listed)
+
+
+def test_noalloc_row_block_matches_workspace_entry_point(device):
+    """The row-block kernel (work lists planned for the XCDs only) through
+    both entry points."""
+    compare_entry_points(device, torch.bfloat16, 32, 8, 128, "rows", "xcd")
+
+
+def compare_entry_points(device, dtype, hq, hkv, d, kernel, listed):
     g = torch.Generator(device=device).manual_seed(31)
     calls = [[5000, 17, 3000, 1, 2048, 700, 4095, 64, 1500, 333, 2600, 4000],  # up to 40 partitions
              [900, 3, 650]]                                                   # second call: smaller

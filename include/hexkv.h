@@ -48,7 +48,9 @@ enum hexkv_dtype {
 };
 
 /* Attention kernels.  AUTO picks MFMA for 16-bit data with head_dim 64 or
- * 128 and 8+ query heads per KV head, VALU otherwise. */
+ * 128 and 8+ query heads per KV head, VALU otherwise; a work list is planned
+ * and launched with hexkv_attend_plan_kernel's choice, which is ROWS for
+ * AUTO on large calls. */
 enum hexkv_kernel {
   HEXKV_KERNEL_AUTO = 0,
   HEXKV_KERNEL_VALU = 1, /* packed dot products on the vector ALUs     */

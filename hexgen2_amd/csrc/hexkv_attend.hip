@@ -1771,7 +1771,9 @@ static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest, boo
 // Chunk of a row-block list (positions, a multiple of 16).  Each XCD runs
 // its share of the list in order on its 32 CUs, as many workgroups per CU
 // at once as registers and LDS allow (4 for 4 query heads per KV head: 103
-// VGPRs and 33 KB of LDS; 5 otherwise: 84 VGPRs), so the first
+// VGPRs and 33 KB of LDS; 5 otherwise: 84 VGPRs; the build records the
+// compiler's figures and tests/test_kernel_resources.py holds them to
+// these counts), so the first
 // kRowsSlots items of a share start together and each later one starts
 // when a slot frees.  A share is its segments' full chunks (all the same
 // size), then their shorter last pieces from the longest down.  The chunk

@@ -1664,15 +1664,24 @@ static void launch(const AttendArgs &a, dim3 grid, int kind, hipStream_t s) {
 // HB KV heads per item.
 template <typename T, int GQ>
 static int dispatch_rows_hb(int HB, const AttendArgs &a, dim3 grid, hipStream_t s) {
+  // The head blocks rows_block picks: 2 KV heads for grouped queries; 8, 4
+  // or 2 for one query head per KV head.
   constexpr int U = slots<T, 128, GQ>();
-  switch (HB) {
-    case 2: attend_rows_kernel<T, 128, GQ, 2, U><<<grid, kAttThreads, 0, s>>>(a); break;
-    case 4: attend_rows_kernel<T, 128, GQ, 4, U><<<grid, kAttThreads, 0, s>>>(a); break;
-    case 8: attend_rows_kernel<T, 128, GQ, 8, U><<<grid, kAttThreads, 0, s>>>(a); break;
-    case 16: attend_rows_kernel<T, 128, GQ, 16, U><<<grid, kAttThreads, 0, s>>>(a); break;
-    default: return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: head block %d", HB);
+  if (HB == 2) {
+    attend_rows_kernel<T, 128, GQ, 2, U><<<grid, kAttThreads, 0, s>>>(a);
+    return HEXKV_OK;
   }
-  return HEXKV_OK;
+  if constexpr (GQ == 1) {
+    if (HB == 4) {
+      attend_rows_kernel<T, 128, GQ, 4, U><<<grid, kAttThreads, 0, s>>>(a);
+      return HEXKV_OK;
+    }
+    if (HB == 8) {
+      attend_rows_kernel<T, 128, GQ, 8, U><<<grid, kAttThreads, 0, s>>>(a);
+      return HEXKV_OK;
+    }
+  }
+  return fail(HEXKV_EUNSUPPORTED, "hexkv_attend: head block %d with %d query heads per KV head", HB, GQ);
 }
 
 template <typename T>

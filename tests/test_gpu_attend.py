@@ -314,6 +314,8 @@ ROWS_GEOMETRIES = [
     (16, 8, torch.bfloat16),   # group 2
     (8, 4, torch.bfloat16),    # group 2, 2 blocks per row
     (4, 4, torch.float16),     # group 1, 4 KV heads: one block of 4
+    (8, 2, torch.bfloat16),    # group 4, one block of 2 per row
+    (6, 6, torch.float16),     # group 1, 6 KV heads: three blocks of 2
 ]
 
 

@@ -1782,9 +1782,8 @@ static int plan_chunk(int64_t positions, int64_t row_bytes, int64_t longest, boo
 // at once as registers and LDS allow (4 for 4 query heads per KV head: 103
 // VGPRs and 33 KB of LDS; 5 otherwise: 84 VGPRs; the build records the
 // compiler's figures and tests/test_kernel_resources.py holds them to
-// these counts), so the first
-// kRowsSlots items of a share start together and each later one starts
-// when a slot frees.  A share is its segments' full chunks (all the same
+// these counts), so the first 32 x (workgroups per CU) items of a share
+// start together and each later one starts when a slot frees.  A share is its segments' full chunks (all the same
 // size), then their shorter last pieces from the longest down.  The chunk
 // is the smallest one at which no share holds more than 27/32 of its slots
 // in full chunks: the full chunks all start at once, and the slots left

@@ -2101,10 +2101,15 @@ static int attend_launch(const hexkv_attend_params *p, void *workspace, size_t w
                     ? static_cast<uint64_t *>(workspace) : nullptr;
   a.n_xcd = p->work_xcds;
   a.xcd_remap = 0;
-  if (a.items && p->work_xcds > 1 && p->n_work_items % p->work_xcds == 0) {
+  if (a.items && p->work_xcds > 0) {
     int device_xcds = 1;
     if ((rc = stream_xcds(stream, &device_xcds, what)) != HEXKV_OK) return rc;
-    a.xcd_remap = device_xcds % p->work_xcds == 0 ? 1 : 0;
+    // The in-kernel merge needs every item of a split segment on one XCD:
+    // only a list dealt over this device's XCDs puts them there.
+    if (a.seg_count && device_xcds != p->work_xcds)
+      return fail(HEXKV_EINVAL, "%s: a work list planned for %d XCDs merges split rows on one XCD, and this "
+                                "device has %d (hexkv_device_xcds)", what, p->work_xcds, device_xcds);
+    a.xcd_remap = p->work_xcds > 1 && device_xcds % p->work_xcds == 0 && p->n_work_items % p->work_xcds == 0;
   }
   a.lengths_out = p->lengths_out_dev;
   // The status word, where a kernel may raise a flag: lengths read from

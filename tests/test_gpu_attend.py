@@ -6,6 +6,8 @@ row bit-exactly and touch nothing else.  Both score kernels are checked: the
 VALU kernel (every dtype and head_dim) and the MFMA kernel (16-bit,
 head_dim >= 64).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -396,6 +398,40 @@ def test_work_list_same_on_every_stream(device, kernel):
         assert torch.equal(c.view(torch.int16), results[0][1].view(torch.int16))
     check(results[0][0], q, results[0][1], [n + 1 for n in lens], torch.bfloat16)
     assert ops.device_status() & _lib.STATUS_ERRORS == 0
+
+
+def test_list_planned_for_other_xcd_count_is_refused(device):
+    """A split list dealt over another XCD count than the device's would put
+    a segment's items on two XCDs, where the in-kernel merge reads stale
+    partials: hexkv_attend refuses it before launching."""
+    lib = _lib.load()
+    lens = [900, 3000, 40]
+    q, cache = make(len(lens), 3100, 32, 8, 128, torch.bfloat16, 50, device)
+    out = torch.full_like(q, 3.0)
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=device)
+    xcds = ops.device_xcds(0)
+    p = ops._attend_params(q, cache, out, seqlens, 0, max(lens), None, False, None, 128, "valu")
+    p.work_xcds = 4 if xcds != 4 else 2
+    c_lens = (ctypes.c_int32 * len(lens))(*lens)
+    n, mp = ctypes.c_int32(), ctypes.c_int32()
+    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, None, 0, None, 0, ctypes.byref(n), ctypes.byref(mp)),
+               "plan")
+    items = torch.empty((n.value, 8), dtype=torch.int32)
+    parts = torch.empty(len(lens) * 32, dtype=torch.int32)
+    _lib.check(lib.hexkv_attend_plan(ctypes.byref(p), c_lens, ctypes.c_void_p(items.data_ptr()), n.value,
+                                     ctypes.c_void_p(parts.data_ptr()), parts.numel(), ctypes.byref(n),
+                                     ctypes.byref(mp)), "plan")
+    assert mp.value > 1  # split rows: the in-kernel merge would run
+    items_d, parts_d = items.to(device), parts.to(device)
+    p.work_items_dev, p.work_parts_dev = items_d.data_ptr(), parts_d.data_ptr()
+    p.n_work_items, p.work_max_parts = n.value, mp.value
+    need = int(lib.hexkv_attend_workspace_bytes(ctypes.byref(p)))
+    ws = torch.zeros(need, dtype=torch.uint8, device=device)
+    rc = lib.hexkv_attend(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == _lib.HEXKV_EINVAL and b"XCDs" in lib.hexkv_last_error()
+    torch.cuda.synchronize()
+    assert (out == 3.0).all(), "nothing was launched"
 
 
 def test_list_planned_for_another_kernel_is_skipped_and_reported(device):

@@ -251,9 +251,10 @@ typedef struct hexkv_attend_params {
    * count and the list length is a multiple of N (as planned), each
    * workgroup runs the item of its own XCD within its group of N, so index
    * j * N + x always runs on XCD x.  Each workgroup checks its XCD and raises
-   * HEXKV_STATUS_PLACEMENT if a segment's items still met on two.  A split
-   * list (work_max_parts > 1) whose N is not the device's XCD count is
-   * refused (HEXKV_EINVAL): its segments would straddle XCDs. */
+   * HEXKV_STATUS_PLACEMENT if a segment's items still met on two.  A list
+   * whose split segments would merge in the attention kernel and whose N is
+   * not the device's XCD count is refused (HEXKV_EINVAL): its segments
+   * would straddle XCDs. */
   int32_t work_xcds;
   /* Work-list calls with kv_new only, else NULL: row b's new cached length
    * (its attended keys, the appended row included) is stored to

@@ -102,19 +102,24 @@ def test_decode_step_at_full_size(device, name, step):
     want_cache = oracle.append(bits(base), bits(kv_new), pos)
     outs = {}
     ops.device_status()  # start clear
-    for kernel in ("valu", "mfma"):
-        for partition, lens, single in ((0, None, True), (128, None, True), (0, pos, True), (0, pos, False)):
-            mode = (f"{kernel}/{'work list' if lens else 'grid'}/partition {partition or 'auto'}"
-                    + ("" if not lens else "/one launch" if single else "/merge kernel"))
-            for scale, q in qs.items():
-                cache = base.clone()
-                outs[mode, scale] = ops.decode_attention(q, cache, max_seqlen=max(pos) + 1, seqlens=seqlens,
-                                                         kv_new=kv_new, kernel=kernel, partition=partition,
-                                                         lens=lens, single_launch=single)
-                torch.cuda.synchronize()
-                assert np.array_equal(bits(cache), want_cache), f"{mode}: fused append differs"
-                del cache
-            print(f"  {mode}: append bit-exact", flush=True)
+    # both per-head kernels on the grid and on lists, and the library's own
+    # choice on the list the bench decodes with (the row-block kernel at
+    # Llama-3-8B and Llama-2-7B)
+    combos = [(kernel, partition, lens, single) for kernel in ("valu", "mfma")
+              for partition, lens, single in ((0, None, True), (128, None, True), (0, pos, True), (0, pos, False))]
+    combos.append(("auto", 0, pos, True))
+    for kernel, partition, lens, single in combos:
+        mode = (f"{kernel}/{'work list' if lens else 'grid'}/partition {partition or 'auto'}"
+                + ("" if not lens else "/one launch" if single else "/merge kernel"))
+        for scale, q in qs.items():
+            cache = base.clone()
+            outs[mode, scale] = ops.decode_attention(q, cache, max_seqlen=max(pos) + 1, seqlens=seqlens,
+                                                     kv_new=kv_new, kernel=kernel, partition=partition,
+                                                     lens=lens, single_launch=single)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(cache), want_cache), f"{mode}: fused append differs"
+            del cache
+        print(f"  {mode}: append bit-exact", flush=True)
     status = ops.device_status()
     print(f"  device status {status:#x}", flush=True)
     assert status & _lib.STATUS_ERRORS == 0

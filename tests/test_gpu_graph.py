@@ -151,6 +151,53 @@ def test_graph_work_list_replays_match_eager_lists(device, hq, hkv, d, dtype, ke
     assert graph.step == 0
 
 
+def test_work_list_graphs_replayed_on_a_side_stream(device):
+    """Work-list step graphs captured and replayed on a stream of the
+    caller's (whose queue may start dispatching at another XCD than the
+    default stream's) equal the eager calls on the default stream, bit for
+    bit, with the row-block kernel the library picks for a large call."""
+    layers, lens, steps = 2, [3000, 40, 2500, 4029, 2800, 4000, 12, 3900], 3  # 83 MB per call
+    hq, hkv, d, dtype = 32, 8, 128, torch.bfloat16
+    cap = max(lens) + steps + 3
+    max_seqlen = max(lens) + steps
+    g = torch.Generator(device=device).manual_seed(24)
+    cache_e = torch.randn((layers, len(lens), cap, 2, hkv, d), generator=g, device=device).to(dtype)
+    cache_g = cache_e.clone()
+    q = torch.randn((layers, len(lens), 1, hq, d), generator=g, device=device).to(dtype)
+    kv_new = torch.randn((layers, len(lens), 2, hkv, d), generator=g, device=device).to(dtype)
+    out_e = torch.empty((layers, len(lens), 1, hq, d), dtype=dtype, device=device)
+    out_g = torch.empty_like(out_e)
+    pos_e = torch.tensor(lens, dtype=torch.int32, device=device)
+    pos_g = pos_e.clone()
+    host = list(lens)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for l in range(layers):  # loads the kernels before capture (on scratch copies)
+            ops.decode_attention(q[l], cache_e[l].clone(), max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[l],
+                                 lens=host)
+        graph = ops.DecodeStepGraph(q, cache_g, out_g, kv_new, pos_g, max_seqlen, lens=host)
+    torch.cuda.synchronize()
+    lists = graph.lists
+    names = {v: k for k, v in _lib.KERNELS.items()}
+    assert lists.xcds > 0 and set(lists.kernels) == {_lib.KERNELS["rows"]}
+    for step in range(steps - 1):
+        for l in range(layers):
+            ops.decode_attention(q[l], cache_e[l], max_seqlen=max_seqlen, seqlens=pos_e, kv_new=kv_new[l],
+                                 out=out_e[l], lens=host, partition=lists.chunks[step],
+                                 kernel=names[lists.kernels[step]])
+        pos_e.add_(1)
+        host = [n + 1 for n in host]
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pos_g, pos_e), f"step {step}: positions differ"
+        assert torch.equal(cache_g.view(torch.int16), cache_e.view(torch.int16)), f"step {step}: caches differ"
+        assert torch.equal(out_g, out_e), f"step {step}: outputs differ"
+    assert ops.device_status() & _lib.STATUS_ERRORS == 0
+
+
 def test_planning_under_capture_is_refused(device):
     """A work list planned inside graph capture would record a copy from a
     temporary host buffer: decode_attention(lens=...) and AttendPlan(lens=...)

@@ -597,8 +597,9 @@ def main():
     ap.add_argument("--no-formats", action="store_true", help="skip the legacy-format figures")
     ap.add_argument("--no-secondary", action="store_true", help="time only --workload")
     ap.add_argument("--ft", action="store_true", help="add the FasterTransformer-layout figures")
-    ap.add_argument("--kernel", default="auto", choices=("auto", "valu", "mfma"),
-                    help="attention kernel (auto: the library's choice for the workload)")
+    ap.add_argument("--kernel", default="auto", choices=("auto", "valu", "mfma", "rows"),
+                    help="attention kernel (auto: the library's choice for the workload; rows: the "
+                         "row-block kernel, work lists only)")
     ap.add_argument("--grid", action="store_true",
                     help="decode attention over the library's uniform partitions instead of work lists")
     ap.add_argument("--two-launch", action="store_true",

@@ -176,6 +176,13 @@ __device__ __forceinline__ bool begin_work(const AttendArgs &a, Work &w) {
     // the call took 159 us against 150-152 at r = 0 and r = 6.
     unsigned idx = blockIdx.x;
     if (a.xcd_remap) idx = idx - idx % a.n_xcd + static_cast<unsigned>(xcd_id()) % a.n_xcd;
+    // The rotation is shared by the whole launch, so workgroup 0 alone
+    // reports it.  (One device-scope atomic per workgroup, as every split
+    // item once did at its merge, cost ~1 us per call at the Llama-2-70B
+    // TP-8 share whenever the rotation was not 0.)
+    if (a.seg_count && a.n_xcd > 0 && blockIdx.x == 0 && threadIdx.x == 0 &&
+        static_cast<unsigned>(xcd_id()) % a.n_xcd != 0)
+      raise_status(a.status, HEXKV_STATUS_DISPATCH);
     const hexkv_work_item it = a.items[idx];
     // Items come from device memory: one naming a row, head group, partition
     // or positions outside this call's geometry does nothing; one planned
@@ -289,7 +296,6 @@ __device__ __forceinline__ void merge_split(const AttendArgs &a, const Work &w, 
     s_last = arrived == w.nparts - 1;
     if (s_last && old + mine != static_cast<uint64_t>(w.nparts) << (8 * x))
       raise_status(a.status, HEXKV_STATUS_PLACEMENT);
-    if (static_cast<unsigned>(x) % a.n_xcd != blockIdx.x % a.n_xcd) raise_status(a.status, HEXKV_STATUS_DISPATCH);
     if (s_last) __hip_atomic_store(count, static_cast<uint64_t>(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();

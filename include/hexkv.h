@@ -92,9 +92,10 @@ const char *hexkv_last_error(void);
                                           (with kv_new, a new row past that bound was neither written nor attended) */
 #define HEXKV_STATUS_PLACEMENT 4u      /* hexkv_attend: the items of a split segment ran on more than one XCD
                                           (work_xcds > 0), so its in-kernel merge may have read stale partials */
-#define HEXKV_STATUS_DISPATCH 8u       /* hexkv_attend, information only: workgroup i started on another XCD
-                                          than i modulo work_xcds (the queue's dispatch starts elsewhere; the
-                                          items still run on the XCDs they were planned for) */
+#define HEXKV_STATUS_DISPATCH 8u       /* hexkv_attend, information only: workgroup 0 of a list merged in the
+                                          kernel started on an XCD other than 0 modulo work_xcds (the queue's
+                                          dispatch starts elsewhere; the items still run on the XCDs they were
+                                          planned for) */
 #define HEXKV_STATUS_LIST 16u          /* hexkv_attend: a work item planned for another head-group size (another
                                           kernel) was skipped, so its outputs were not written */
 

@@ -198,6 +198,7 @@ def test_work_list_graphs_replayed_on_a_side_stream(device):
     assert ops.device_status() & _lib.STATUS_ERRORS == 0
 
 
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")  # the refused capture records nothing
 def test_planning_under_capture_is_refused(device):
     """A work list planned inside graph capture would record a copy from a
     temporary host buffer: decode_attention(lens=...) and AttendPlan(lens=...)

@@ -11,8 +11,9 @@
 //    crosses at most a few sequence boundaries, found by one scalar binary
 //    search per workgroup;
 //  * each lane moves 16-byte vectors with nontemporal (streaming) loads and
-//    stores, eight in flight per lane, so the 256 MB MALL is not polluted by
-//    data that is touched exactly once.
+//    stores, eight in flight per lane (four in the 256-thread workgroups of
+//    copies below 128 MB), so the 256 MB MALL is not polluted by data that
+//    is touched exactly once.
 #include "hexkv_common.h"
 
 #include <algorithm>
@@ -33,6 +34,14 @@ namespace hexkv {
 // read-only stream 7.1.
 constexpr int kCopyThreads = 1024;
 constexpr int kCopyUnroll = 8;
+// Copies below 128 MB (16 KB chunks, the smallest; TinyLlama's 22-layer
+// handoff moves 11.5 MB each way) run 256 threads x 4 vectors: the same 16 KB
+// per workgroup, all of it loaded before any store, and a quarter of the
+// threads, so the grid is resident at once instead of in two rounds of
+// 1024-thread workgroups.
+constexpr int kSmallCopyThreads = 256;
+constexpr int kSmallCopyUnroll = 4;
+constexpr int64_t kSmallCopyChunk = INT64_C(16384);
 // The per-step append moves one row per sequence: 512 threads, one vector each.
 constexpr int kAppendThreads = 512;
 
@@ -59,36 +68,36 @@ using WideCopyArgs = RaggedCopyArgs<HEXKV_MAX_LAYERS_PER_LAUNCH, HEXKV_MAX_SEQS_
 using SmallCopyArgs = RaggedCopyArgs<32, 16>;
 static_assert(sizeof(WideCopyArgs) <= 4096, "kernel arguments above 4 KiB");
 
-// Every pass issues kCopyUnroll loads per lane before its stores; the last,
+// Every pass issues UN loads per lane (NT lanes) before its stores; the last,
 // partial pass masks lanes instead of falling back to one vector at a time.
-template <typename V>
+template <typename V, int NT, int UN>
 __device__ __forceinline__ void copy_span(const char *__restrict__ s, char *__restrict__ d,
                                           int64_t n) {
   const V *sv = reinterpret_cast<const V *>(s);
   V *dv = reinterpret_cast<V *>(d);
   const int64_t nv = n / static_cast<int64_t>(sizeof(V));
   int64_t i = threadIdx.x;
-  for (; i + (kCopyUnroll - 1) * kCopyThreads < nv; i += kCopyUnroll * kCopyThreads) {
-    V r[kCopyUnroll];
+  for (; i + (UN - 1) * NT < nv; i += UN * NT) {
+    V r[UN];
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) r[u] = __builtin_nontemporal_load(sv + i + u * kCopyThreads);
+    for (int u = 0; u < UN; ++u) r[u] = __builtin_nontemporal_load(sv + i + u * NT);
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) __builtin_nontemporal_store(r[u], dv + i + u * kCopyThreads);
+    for (int u = 0; u < UN; ++u) __builtin_nontemporal_store(r[u], dv + i + u * NT);
   }
   if (i < nv) {
-    V r[kCopyUnroll];
+    V r[UN];
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u)
-      if (i + u * kCopyThreads < nv) r[u] = __builtin_nontemporal_load(sv + i + u * kCopyThreads);
+    for (int u = 0; u < UN; ++u)
+      if (i + u * NT < nv) r[u] = __builtin_nontemporal_load(sv + i + u * NT);
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u)
-      if (i + u * kCopyThreads < nv) __builtin_nontemporal_store(r[u], dv + i + u * kCopyThreads);
+    for (int u = 0; u < UN; ++u)
+      if (i + u * NT < nv) __builtin_nontemporal_store(r[u], dv + i + u * NT);
   }
 }
 
 // PACK: src = padded cache, dst = packed buffer.  UNPACK: the reverse.
-template <typename V, bool PACK, typename A>
-__global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const A a) {
+template <typename V, bool PACK, typename A, int NT, int UN>
+__global__ __launch_bounds__(NT) void ragged_copy_kernel(const A a) {
   const int64_t start = static_cast<int64_t>(blockIdx.x) * a.chunk_bytes;
   if (start >= a.layer_bytes) return;
   const int64_t end = min(start + a.chunk_bytes, a.layer_bytes);
@@ -108,8 +117,8 @@ __global__ __launch_bounds__(kCopyThreads) void ragged_copy_kernel(const A a) {
     const int64_t p0 = max(start, seg0), p1 = min(end, seg1);
     if (p0 >= p1) continue;
     const int64_t padded = static_cast<int64_t>(b) * a.seq_stride_bytes + (p0 - seg0);
-    if constexpr (PACK) copy_span<V>(src + padded, dst + p0, p1 - p0);
-    else copy_span<V>(src + p0, dst + padded, p1 - p0);
+    if constexpr (PACK) copy_span<V, NT, UN>(src + padded, dst + p0, p1 - p0);
+    else copy_span<V, NT, UN>(src + p0, dst + padded, p1 - p0);
   }
 }
 
@@ -155,7 +164,7 @@ int status_word(hexkv_stream_t stream, unsigned int **word, const char *what) {
 static int64_t choose_chunk(int64_t total_bytes) {
   const int64_t target_wgs = 8192;
   int64_t chunk = (total_bytes / target_wgs + 4095) / 4096 * 4096;
-  return std::min<int64_t>(std::max<int64_t>(chunk, 16384), 131072);
+  return std::min<int64_t>(std::max<int64_t>(chunk, kSmallCopyChunk), 131072);
 }
 
 // One launch: layers [l0, l0 + nl) of sequences [b0, b0 + nb), whose packed
@@ -181,12 +190,18 @@ static int launch_copy(bool pack, bool vec16, const void *const *src_layers, voi
   const int64_t gx = (a.layer_bytes + chunk - 1) / chunk;
   if (gx > INT32_MAX) return fail(HEXKV_ERANGE, "%s: grid too large", what);
   dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(nl));
-  if (vec16) {
-    if (pack) ragged_copy_kernel<u32x4, true, A><<<grid, kCopyThreads, 0, stream>>>(a);
-    else ragged_copy_kernel<u32x4, false, A><<<grid, kCopyThreads, 0, stream>>>(a);
+  if (vec16 && chunk == kSmallCopyChunk) {
+    constexpr int NT = kSmallCopyThreads, UN = kSmallCopyUnroll;
+    if (pack) ragged_copy_kernel<u32x4, true, A, NT, UN><<<grid, NT, 0, stream>>>(a);
+    else ragged_copy_kernel<u32x4, false, A, NT, UN><<<grid, NT, 0, stream>>>(a);
+  } else if (vec16) {
+    constexpr int NT = kCopyThreads, UN = kCopyUnroll;
+    if (pack) ragged_copy_kernel<u32x4, true, A, NT, UN><<<grid, NT, 0, stream>>>(a);
+    else ragged_copy_kernel<u32x4, false, A, NT, UN><<<grid, NT, 0, stream>>>(a);
   } else {
-    if (pack) ragged_copy_kernel<unsigned int, true, A><<<grid, kCopyThreads, 0, stream>>>(a);
-    else ragged_copy_kernel<unsigned int, false, A><<<grid, kCopyThreads, 0, stream>>>(a);
+    constexpr int NT = kCopyThreads, UN = kCopyUnroll;
+    if (pack) ragged_copy_kernel<unsigned int, true, A, NT, UN><<<grid, NT, 0, stream>>>(a);
+    else ragged_copy_kernel<unsigned int, false, A, NT, UN><<<grid, NT, 0, stream>>>(a);
   }
   return check_launch(what);
 }

@@ -635,16 +635,20 @@ def ft_attend(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, k_cache
 
 def _tensor_geometry(t: Optional[torch.Tensor]):
     """Everything about a tensor a prebuilt parameter block depends on apart
-    from its address: shape, strides, dtype, device and contiguity."""
+    from its address: shape, strides (which fix its contiguity), dtype and
+    device.  A GPU tensor's device is its index (``get_device``, cheap: this
+    key is built on every ``AttendPlan`` call), any other tensor's its
+    device type."""
     if t is None:
         return None
-    return tuple(t.shape), t.stride(), t.dtype, t.device, t.is_contiguous()
+    dev = t.get_device()
+    return t.shape, t.stride(), t.dtype, dev if dev >= 0 else t.device.type
 
 
 def _plan_geometry(q, cache, out, kv_new) -> tuple:
     """The key an ``AttendPlan`` compares per call: the geometry of q, cache,
     out and kv_new (None when the call has no fused append)."""
-    return tuple(_tensor_geometry(t) for t in (q, cache, out, kv_new))
+    return _tensor_geometry(q), _tensor_geometry(cache), _tensor_geometry(out), _tensor_geometry(kv_new)
 
 
 def _check_plan_geometry(want: tuple, got: tuple) -> None:
